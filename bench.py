@@ -1,0 +1,218 @@
+"""Benchmark of the DSA decode hot path on one MI355X.
+
+Default workload ("C3"): DeepSeek-V3.2-shape decode
+at 131072-token context, batch 1, one TP-8 share (16 attention heads, the
+full 64x128 indexer), two consecutive layers under the MLI lag schedule --
+layer L attends layer L-1's top-2048 while layer L's indexer runs on a
+second stream -- captured as one hipGraph.  A step is one replay of that
+graph (2 layers).  Inputs are synthetic N(0,1) (fp8 caches, seeded random
+page table of 64-token pages) and resident in HBM before timing starts.
+
+Prints ONE JSON line.  value = microseconds per decode layer (lower is
+better).  Extra fields: tokens/s, indexer-scan GB/s, the MLI hidden
+fraction, the roofline of the dominant kernel (the indexer scan, timed with
+HIP events per launch on its own stream) and the CPU baseline (the
+reference's fp32 decode-row path restated in oracle/, timed on this host).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "dsa-multi-layer-indexer_amd"))
+sys.path.insert(0, str(REPO))
+
+HBM_PEAK_GBS = 8000.0
+CONFIGS = {
+    "c2": dict(lens=[32768], layers=2, indexer_every=1, desc="v32_ctx32768_b1_2layer_mli_graph"),
+    "c3": dict(lens=[131072], layers=2, indexer_every=1, desc="v32_ctx131072_b1_2layer_mli_graph"),
+    "c4": dict(lens=None, layers=2, indexer_every=1, desc="v32_varlen32_ctx16k-128k_2layer_mli_graph"),
+    "c5": dict(lens=[196608], layers=61, indexer_every=4, desc="v32_ctx196608_b1_61layer_indexcache4_mli_graph"),
+}
+
+
+def scan_bytes(lens: list[int], hidx: int = 64) -> int:
+    """Algorithmic HBM bytes of one scan launch: 128 B key + 4 B scale read
+    and 4 B score written per token, the fp8 query, the weights and the
+    page-table entries."""
+    tok = sum(lens)
+    pages = sum((n + 63) // 64 for n in lens)
+    return 136 * tok + len(lens) * (hidx * 128 + hidx * 4) + 4 * pages
+
+
+def attn_bytes(B: int, topk: int = 2048, H: int = 16) -> int:
+    """Gathered latent rows + bf16 query + bf16 output per row."""
+    return B * (topk * 656 + H * 576 * 2 + H * 512 * 2)
+
+
+def time_graph(fn, iters: int, torch) -> float:
+    """Average ms of fn() over iters, bracketed by synchronize."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / iters
+
+
+def event_ms(fn, iters: int, torch) -> float:
+    """Average per-launch device time of fn() with HIP events recorded on the
+    stream fn launches on (torch's current stream)."""
+    pairs = []
+    for _ in range(iters):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        pairs.append((a, b))
+    torch.cuda.synchronize()
+    return statistics.mean(a.elapsed_time(b) for a, b in pairs)
+
+
+def cpu_baseline(ctx: int, budget_s: float = 15.0) -> dict:
+    """The reference's fp32 decode-row path (oracle/cpu_reference_path.py) on
+    this host's cores, bounded to about budget_s seconds."""
+    import torch
+
+    from oracle.cpu_reference_path import decode_layer_fp32, make_inputs
+
+    inp = make_inputs(ctx, seed=0)
+    decode_layer_fp32(*inp, topk=2048)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        decode_layer_fp32(*inp, topk=2048)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 50:
+            break
+    return {"value": statistics.median(times) * 1e6, "unit": "us/layer",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{len(times)} fp32 decode layers (indexer_logits -> select_topk -> "
+                      f"masked _attend) at ctx {ctx}, b=1, median"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only (one TP-8 share of heads); "
+                                   "multi-GPU runs are not part of it", "n_gpus": args.gpus}))
+        return 2
+
+    import torch
+
+    from lagged_indexer_dsa_amd import ops
+    from lagged_indexer_dsa_amd import synthetic as S
+    from lagged_indexer_dsa_amd.decode import MLISchedule
+
+    dev = torch.device("cuda:0")
+    cfg = CONFIGS[args.config]
+    lens = cfg["lens"]
+    if lens is None:
+        g = torch.Generator().manual_seed(4000)
+        lens = torch.randint(16384, 131073, (32,), generator=g).tolist()
+    B = len(lens)
+    n_layers = cfg["layers"]
+    pt, num_pages = S.make_page_table(lens, seed=1000, device=dev)
+    layers = [S.make_decode_layer(lens, seed=1000 * 3 + i, device=dev, page_table=pt,
+                                  num_pages=num_pages, indexer=(i % cfg["indexer_every"] == 0))
+              for i in range(n_layers)]
+    first = S.random_selection(lens, 2048, pt, seed=7, device=dev)
+    torch.cuda.synchronize()
+
+    full = MLISchedule(layers, first)
+    attn_only = MLISchedule(layers, first, indexer=False, attend_all_first=True)
+    idx_only = MLISchedule(layers, first, attention=False)
+    for s in (full, attn_only, idx_only):
+        s.capture()
+
+    for _ in range(args.warmup):
+        full.replay()
+    # ---- timed region: exactly `steps` graph replays ----
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        full.replay()
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    reps = max(20, args.steps // 2)
+    t_attn = time_graph(attn_only.replay, reps, torch)
+    t_idx = time_graph(idx_only.replay, reps, torch)
+    t_full = time_graph(full.replay, reps, torch)
+    hidden = 1.0 - (t_full - t_attn) / t_idx if t_idx > 0 else None
+
+    # ---- dominant kernel: indexer scan, per-launch HIP events ----
+    L0 = layers[0]
+    scan = lambda: ops.indexer_scan(L0.q_fp8, L0.w, L0.index_k, L0.page_table, L0.seq_lens,
+                                    L0.slab_stride, out=L0.scores)
+    for _ in range(10):
+        scan()
+    scan_ms = event_ms(scan, 200, torch)
+    sb = scan_bytes(lens)
+    scan_gbs = sb / (scan_ms * 1e-3) / 1e9
+    topk_fn = lambda: ops.topk(L0.scores, L0.seq_lens, 2048, page_table=L0.page_table,
+                               out=L0.next_idx)
+    topk_ms = event_ms(topk_fn, 100, torch)
+    attn_fn = lambda: ops.sparse_mla_decode(L0.q_bf16, L0.kv_pool, first, workspace=L0.workspace,
+                                            out=L0.out)
+    attn_ms = event_ms(attn_fn, 100, torch)
+    ab = attn_bytes(B)
+
+    us_layer = ms_step * 1e3 / n_layers
+    res = {
+        "metric": ("\u00b5s per DSA decode layer at 128K ctx (b=1, 16 heads); indexer-scan HBM GB/s"
+                   if args.config == "c3" else f"\u00b5s per DSA decode layer ({args.config})"),
+        "value": round(us_layer, 3),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8e4m3-indexer/fp8-kv-bf16-mla/fp32-accum",
+        "data": "synthetic N(0,1), seeded, fp8-quantised paged caches (64-token pages, random page table)",
+        "config": {"workload": cfg["desc"], "batch": B, "ctx": lens if B <= 4 else
+                   {"min": min(lens), "max": max(lens), "sum": sum(lens)},
+                   "layers_per_step": n_layers, "index_heads": 64, "attn_heads": 16,
+                   "topk": 2048, "page_tokens": 64, "schedule": "MLI lag, 2 streams, 1 hipGraph"},
+        "tokens_per_s": round(B / (us_layer * 1e-6), 1),
+        "indexer_scan_GBps": round(scan_gbs, 1),
+        "kernel_us": {"indexer_scan": round(scan_ms * 1e3, 3), "topk": round(topk_ms * 1e3, 3),
+                      "sparse_mla+combine": round(attn_ms * 1e3, 3)},
+        "attention_gather_GBps": round(ab / (attn_ms * 1e-3) / 1e9, 1),
+        "mli": {"graph_ms": round(t_full, 5), "attn_only_ms": round(t_attn, 5),
+                "indexer_only_ms": round(t_idx, 5),
+                "hidden_fraction": None if hidden is None else round(hidden, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(scan_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(scan_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "indexer_scan_kernel",
+                     "algorithmic_bytes": sb},
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(131072 if args.config == "c3" else 8192, args.cpu_budget)
+    for s in (full, attn_only, idx_only):
+        s.close()
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

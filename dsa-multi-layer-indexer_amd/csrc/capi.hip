@@ -1,0 +1,342 @@
+// C ABI of libdsa_mli.so: argument contracts, the decode-layer composite and
+// the MLI two-stream schedule (eager and captured as one hipGraph).
+//
+// Contract checks mirror the reference launcher's TORCH_CHECKs
+// (kernels/cuda_fused_sparse_splitk.py K:2399-2611) as negative return codes;
+// nothing is launched when a check fails.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "dsa_common.h"
+
+namespace dsa {
+hipError_t launch_indexer_scan(const uint8_t* q8, const float* w, const uint8_t* pages,
+                               long num_pages, const int* pt, const int* seq_lens, float* scores,
+                               int B, int Hidx, int pt_stride, int slab_stride, hipStream_t s);
+void set_scan_variant(int v);
+hipError_t launch_topk(const float* scores, const int* seq_lens, const int* page_table,
+                       int pt_stride, int* out, int B, int slab_stride, int K, int sorted,
+                       int pad, hipStream_t s);
+hipError_t launch_sparse_mla(const uint16_t* q, const uint8_t* pool, long kv_rows,
+                             const int* idx, void* workspace, uint16_t* out, int B, int H,
+                             int topk, int nsplit, float sm_scale, hipStream_t s);
+int sparse_mla_auto_nsplit(int topk);
+size_t sparse_mla_workspace_bytes(int B, int H, int nsplit);
+}  // namespace dsa
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return DSA_OK;
+  return fail(DSA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define DSA_REQUIRE(cond, code, ...) \
+  do {                               \
+    if (!(cond)) return fail(code, __VA_ARGS__); \
+  } while (0)
+
+int check_scan(const void* q_fp8, const float* w, const void* index_k, int64_t num_pages,
+               const int32_t* page_table, const int32_t* seq_lens, const float* scores, int B,
+               int Hidx, int pt_stride, int slab_stride) {
+  DSA_REQUIRE(q_fp8 && w && index_k && page_table && seq_lens && scores, DSA_ERR_INVALID_ARG,
+              "dsa_indexer_scan: null pointer argument");
+  DSA_REQUIRE(B >= 1, DSA_ERR_INVALID_ARG, "dsa_indexer_scan: B must be >= 1 (got %d)", B);
+  DSA_REQUIRE(B <= 65535, DSA_ERR_UNSUPPORTED, "dsa_indexer_scan: B must be <= 65535");
+  DSA_REQUIRE(Hidx >= 16 && Hidx <= 64 && Hidx % 16 == 0, DSA_ERR_UNSUPPORTED,
+              "dsa_indexer_scan: index_n_heads must be 16, 32, 48 or 64 (got %d)", Hidx);
+  DSA_REQUIRE(num_pages >= 1, DSA_ERR_INVALID_ARG, "dsa_indexer_scan: num_pages must be >= 1");
+  DSA_REQUIRE(pt_stride >= 1, DSA_ERR_INVALID_ARG, "dsa_indexer_scan: pt_stride must be >= 1");
+  DSA_REQUIRE(slab_stride >= 1, DSA_ERR_INVALID_ARG, "dsa_indexer_scan: slab_stride must be >= 1");
+  DSA_REQUIRE(((uintptr_t)q_fp8 & 15) == 0 && ((uintptr_t)index_k & 15) == 0,
+              DSA_ERR_INVALID_ARG, "dsa_indexer_scan: q_fp8 and index_k must be 16-byte aligned");
+  return DSA_OK;
+}
+
+int check_topk(const float* scores, const int32_t* seq_lens, const int32_t* page_table,
+               int pt_stride, const int32_t* out_idx, int B, int slab_stride, int topk,
+               int flags) {
+  DSA_REQUIRE(scores && seq_lens && out_idx, DSA_ERR_INVALID_ARG, "dsa_topk: null pointer argument");
+  DSA_REQUIRE(B >= 1, DSA_ERR_INVALID_ARG, "dsa_topk: B must be >= 1 (got %d)", B);
+  DSA_REQUIRE(topk >= 1, DSA_ERR_INVALID_ARG, "dsa_topk: topk must be >= 1 (got %d)", topk);
+  DSA_REQUIRE(flags == DSA_TOPK_POSITION_ORDER || flags == DSA_TOPK_SORTED, DSA_ERR_INVALID_ARG,
+              "dsa_topk: unknown flags %d", flags);
+  DSA_REQUIRE(topk <= (flags == DSA_TOPK_SORTED ? 4096 : 8192), DSA_ERR_UNSUPPORTED,
+              "dsa_topk: topk %d above the supported maximum", topk);
+  DSA_REQUIRE(slab_stride >= 1 && slab_stride <= DSA_TOPK_MAX_CTX, DSA_ERR_UNSUPPORTED,
+              "dsa_topk: slab_stride must be in [1, %d] (got %d)", DSA_TOPK_MAX_CTX, slab_stride);
+  DSA_REQUIRE(page_table == nullptr || flags == DSA_TOPK_POSITION_ORDER, DSA_ERR_INVALID_ARG,
+              "dsa_topk: page-table slot mapping requires DSA_TOPK_POSITION_ORDER");
+  DSA_REQUIRE(page_table == nullptr || (int64_t)pt_stride * DSA_PAGE_TOKENS >= slab_stride,
+              DSA_ERR_INVALID_ARG, "dsa_topk: page table must cover slab_stride (pt_stride*64 >= slab_stride)");
+  return DSA_OK;
+}
+
+int check_mla(const void* q_bf16, const void* kv_pool, int64_t kv_rows, const int32_t* idx,
+              const void* workspace, const void* out_bf16, int B, int H, int topk, int nsplit) {
+  DSA_REQUIRE(q_bf16 && kv_pool && idx && workspace && out_bf16, DSA_ERR_INVALID_ARG,
+              "dsa_sparse_mla_decode: null pointer argument");
+  DSA_REQUIRE(B >= 1 && B <= 65535, DSA_ERR_INVALID_ARG, "dsa_sparse_mla_decode: bad B %d", B);
+  DSA_REQUIRE(H >= 16 && H % 16 == 0 && H <= 16 * 64, DSA_ERR_UNSUPPORTED,
+              "dsa_sparse_mla_decode: H must be a positive multiple of 16 (got %d)", H);
+  DSA_REQUIRE(topk >= 1, DSA_ERR_INVALID_ARG, "dsa_sparse_mla_decode: topk must be >= 1");
+  DSA_REQUIRE(nsplit >= 0 && nsplit <= 128, DSA_ERR_UNSUPPORTED,
+              "dsa_sparse_mla_decode: nsplit must be in [0, 128] (got %d)", nsplit);
+  DSA_REQUIRE(kv_rows >= 1, DSA_ERR_INVALID_ARG, "dsa_sparse_mla_decode: kv_rows must be >= 1");
+  DSA_REQUIRE(((uintptr_t)q_bf16 & 15) == 0 && ((uintptr_t)kv_pool & 15) == 0 &&
+                  ((uintptr_t)workspace & 15) == 0 && ((uintptr_t)out_bf16 & 7) == 0,
+              DSA_ERR_INVALID_ARG, "dsa_sparse_mla_decode: q/kv_pool/workspace must be 16-byte aligned");
+  return DSA_OK;
+}
+
+int resolve_nsplit(int nsplit, int topk) {
+  return nsplit > 0 ? nsplit : dsa::sparse_mla_auto_nsplit(topk);
+}
+
+int check_layer(const dsa_layer_args* a) {
+  DSA_REQUIRE(a != nullptr, DSA_ERR_INVALID_ARG, "dsa_layer_args is null");
+  int rc;
+  if (a->q_fp8) {
+    rc = check_scan(a->q_fp8, a->w, a->index_k, a->num_idx_pages, a->page_table, a->seq_lens,
+                    a->scores, a->B, a->Hidx, a->pt_stride, a->slab_stride);
+    if (rc) return rc;
+    rc = check_topk(a->scores, a->seq_lens, a->page_table, a->pt_stride, a->next_idx, a->B,
+                    a->slab_stride, a->topk, DSA_TOPK_POSITION_ORDER);
+    if (rc) return rc;
+  }
+  if (a->q_bf16) {
+    const int32_t* att = a->attend_idx ? a->attend_idx : a->next_idx;
+    DSA_REQUIRE(a->attend_idx || a->q_fp8, DSA_ERR_INVALID_ARG,
+                "dsa_decode_layer: attention needs attend_idx or an indexer");
+    rc = check_mla(a->q_bf16, a->kv_pool, a->kv_rows, att, a->workspace, a->out_bf16, a->B, a->H,
+                   a->topk, a->nsplit);
+    if (rc) return rc;
+  }
+  return DSA_OK;
+}
+
+int enqueue_indexer(const dsa_layer_args* a, hipStream_t s) {
+  int rc = hip_status(
+      dsa::launch_indexer_scan((const uint8_t*)a->q_fp8, a->w, (const uint8_t*)a->index_k,
+                               (long)a->num_idx_pages, a->page_table, a->seq_lens, a->scores, a->B,
+                               a->Hidx, a->pt_stride, a->slab_stride, s),
+      "indexer scan launch");
+  if (rc) return rc;
+  return hip_status(dsa::launch_topk(a->scores, a->seq_lens, a->page_table, a->pt_stride,
+                                     a->next_idx, a->B, a->slab_stride, a->topk, 0, -1, s),
+                    "top-k launch");
+}
+
+int enqueue_attention(const dsa_layer_args* a, const int32_t* att, hipStream_t s) {
+  return hip_status(
+      dsa::launch_sparse_mla((const uint16_t*)a->q_bf16, (const uint8_t*)a->kv_pool,
+                             (long)a->kv_rows, att, a->workspace, (uint16_t*)a->out_bf16, a->B,
+                             a->H, a->topk, resolve_nsplit(a->nsplit, a->topk), a->sm_scale, s),
+      "sparse MLA launch");
+}
+
+// Enqueue the MLI schedule: attention on `main`, indexers on `side`.
+//   indexer(i) waits for attention(i-1) (its query comes from layer i's input);
+//   attention(i) waits for the indexer whose selection it consumes.
+int enqueue_mli(const dsa_layer_args* layers, int n, hipStream_t main, hipStream_t side,
+                std::vector<hipEvent_t>& events) {
+  auto new_event = [&](hipEvent_t* e) -> int {
+    hipError_t err = hipEventCreateWithFlags(e, hipEventDisableTiming);
+    if (err != hipSuccess) return hip_status(err, "hipEventCreate");
+    events.push_back(*e);
+    return DSA_OK;
+  };
+  int rc;
+  const int32_t* carried = nullptr;   // selection available to the next layer
+  hipEvent_t carried_ev = nullptr;     // side-stream event that produced it
+  hipEvent_t side_tail = nullptr;      // last event recorded on side
+  for (int i = 0; i < n; ++i) {
+    const dsa_layer_args* a = &layers[i];
+    const int32_t* att = a->attend_idx ? a->attend_idx : carried;
+    hipEvent_t att_ev = a->attend_idx ? nullptr : carried_ev;
+    if (a->q_fp8) {
+      hipEvent_t fork;
+      if ((rc = new_event(&fork))) return rc;
+      if ((rc = hip_status(hipEventRecord(fork, main), "hipEventRecord"))) return rc;
+      if ((rc = hip_status(hipStreamWaitEvent(side, fork, 0), "hipStreamWaitEvent"))) return rc;
+      if ((rc = enqueue_indexer(a, side))) return rc;
+      hipEvent_t done;
+      if ((rc = new_event(&done))) return rc;
+      if ((rc = hip_status(hipEventRecord(done, side), "hipEventRecord"))) return rc;
+      carried = a->next_idx;
+      carried_ev = done;
+      side_tail = done;
+    }
+    if (a->q_bf16) {
+      if (!att) return fail(DSA_ERR_INVALID_ARG, "mli layer %d: no selection to attend", i);
+      if (att_ev && (rc = hip_status(hipStreamWaitEvent(main, att_ev, 0), "hipStreamWaitEvent")))
+        return rc;
+      if ((rc = enqueue_attention(a, att, main))) return rc;
+    }
+  }
+  // join the side stream back so the schedule ends on `main`
+  if (side_tail && (rc = hip_status(hipStreamWaitEvent(main, side_tail, 0), "hipStreamWaitEvent")))
+    return rc;
+  return DSA_OK;
+}
+
+}  // namespace
+
+struct dsa_mli_graph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  hipStream_t side = nullptr;
+  std::vector<hipEvent_t> events;
+};
+
+extern "C" {
+
+const char* dsa_last_error(void) { return g_err; }
+
+const char* dsa_version(void) { return "dsa_mli 0.1.0 gfx950"; }
+
+int dsa_indexer_scan(const void* q_fp8, const float* w, const void* index_k, int64_t num_pages,
+                     const int32_t* page_table, const int32_t* seq_lens, float* scores, int B,
+                     int Hidx, int pt_stride, int slab_stride, void* stream) {
+  int rc = check_scan(q_fp8, w, index_k, num_pages, page_table, seq_lens, scores, B, Hidx,
+                      pt_stride, slab_stride);
+  if (rc) return rc;
+  return hip_status(dsa::launch_indexer_scan((const uint8_t*)q_fp8, w, (const uint8_t*)index_k,
+                                             (long)num_pages, page_table, seq_lens, scores, B,
+                                             Hidx, pt_stride, slab_stride, (hipStream_t)stream),
+                    "indexer scan launch");
+}
+
+int dsa_topk(const float* scores, const int32_t* seq_lens, const int32_t* page_table,
+             int pt_stride, int32_t* out_idx, int B, int slab_stride, int topk, int flags,
+             int32_t pad_value, void* stream) {
+  int rc = check_topk(scores, seq_lens, page_table, pt_stride, out_idx, B, slab_stride, topk, flags);
+  if (rc) return rc;
+  return hip_status(dsa::launch_topk(scores, seq_lens, page_table, pt_stride, out_idx, B,
+                                     slab_stride, topk, flags == DSA_TOPK_SORTED, pad_value,
+                                     (hipStream_t)stream),
+                    "top-k launch");
+}
+
+size_t dsa_sparse_mla_workspace_bytes(int B, int H, int nsplit) {
+  if (B < 1 || H < 16 || H % 16 || nsplit < 0 || nsplit > 128) return 0;
+  return dsa::sparse_mla_workspace_bytes(B, H, nsplit > 0 ? nsplit : 128);
+}
+
+int dsa_sparse_mla_decode(const void* q_bf16, const void* kv_pool, int64_t kv_rows,
+                          const int32_t* idx, void* workspace, void* out_bf16, int B, int H,
+                          int topk, int nsplit, float sm_scale, void* stream) {
+  int rc = check_mla(q_bf16, kv_pool, kv_rows, idx, workspace, out_bf16, B, H, topk, nsplit);
+  if (rc) return rc;
+  return hip_status(dsa::launch_sparse_mla((const uint16_t*)q_bf16, (const uint8_t*)kv_pool,
+                                           (long)kv_rows, idx, workspace, (uint16_t*)out_bf16, B,
+                                           H, topk, resolve_nsplit(nsplit, topk), sm_scale,
+                                           (hipStream_t)stream),
+                    "sparse MLA launch");
+}
+
+int dsa_decode_layer(const dsa_layer_args* args, void* stream) {
+  int rc = check_layer(args);
+  if (rc) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  if (args->q_fp8 && (rc = enqueue_indexer(args, s))) return rc;
+  if (args->q_bf16)
+    return enqueue_attention(args, args->attend_idx ? args->attend_idx : args->next_idx, s);
+  return DSA_OK;
+}
+
+static int check_mli(const dsa_layer_args* layers, int n) {
+  DSA_REQUIRE(layers && n >= 1, DSA_ERR_INVALID_ARG, "mli: need at least one layer");
+  const int32_t* carried = nullptr;
+  for (int i = 0; i < n; ++i) {
+    int rc = check_layer(&layers[i]);
+    if (rc) return rc;
+    if (layers[i].q_bf16 && !layers[i].attend_idx && !carried)
+      return fail(DSA_ERR_INVALID_ARG, "mli layer %d: attend_idx is NULL and no earlier layer indexes", i);
+    if (layers[i].q_fp8) carried = layers[i].next_idx;
+  }
+  return DSA_OK;
+}
+
+int dsa_mli_run_eager(const dsa_layer_args* layers, int num_layers, void* stream,
+                      void* side_stream) {
+  int rc = check_mli(layers, num_layers);
+  if (rc) return rc;
+  DSA_REQUIRE(side_stream && side_stream != stream, DSA_ERR_INVALID_ARG,
+              "dsa_mli_run_eager: side_stream must be a distinct non-null stream");
+  std::vector<hipEvent_t> events;
+  rc = enqueue_mli(layers, num_layers, (hipStream_t)stream, (hipStream_t)side_stream, events);
+  for (hipEvent_t e : events) (void)hipEventDestroy(e);
+  return rc;
+}
+
+int dsa_mli_graph_create(const dsa_layer_args* layers, int num_layers, void* capture_stream,
+                         dsa_mli_graph** out_graph) {
+  DSA_REQUIRE(out_graph, DSA_ERR_INVALID_ARG, "dsa_mli_graph_create: out_graph is null");
+  *out_graph = nullptr;
+  int rc = check_mli(layers, num_layers);
+  if (rc) return rc;
+  hipStream_t main = (hipStream_t)capture_stream;
+  bool own_main = false;
+  if (main == nullptr) {
+    if ((rc = hip_status(hipStreamCreateWithFlags(&main, hipStreamNonBlocking), "hipStreamCreate")))
+      return rc;
+    own_main = true;
+  }
+  dsa_mli_graph* g = new dsa_mli_graph();
+  rc = hip_status(hipStreamCreateWithFlags(&g->side, hipStreamNonBlocking), "hipStreamCreate");
+  if (!rc) rc = hip_status(hipStreamBeginCapture(main, hipStreamCaptureModeThreadLocal),
+                           "hipStreamBeginCapture");
+  if (!rc) {
+    int erc = enqueue_mli(layers, num_layers, main, g->side, g->events);
+    hipGraph_t graph = nullptr;
+    int crc = hip_status(hipStreamEndCapture(main, &graph), "hipStreamEndCapture");
+    rc = erc ? erc : crc;
+    g->graph = graph;
+    if (!rc) rc = hip_status(hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0),
+                             "hipGraphInstantiate");
+  }
+  if (own_main) (void)hipStreamDestroy(main);
+  if (rc) {
+    dsa_mli_graph_destroy(g);
+    return rc;
+  }
+  *out_graph = g;
+  return DSA_OK;
+}
+
+int dsa_mli_graph_launch(dsa_mli_graph* graph, void* stream) {
+  DSA_REQUIRE(graph && graph->exec, DSA_ERR_INVALID_ARG, "dsa_mli_graph_launch: invalid graph");
+  return hip_status(hipGraphLaunch(graph->exec, (hipStream_t)stream), "hipGraphLaunch");
+}
+
+int dsa_mli_graph_destroy(dsa_mli_graph* graph) {
+  if (!graph) return DSA_OK;
+  if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
+  if (graph->graph) (void)hipGraphDestroy(graph->graph);
+  for (hipEvent_t e : graph->events) (void)hipEventDestroy(e);
+  if (graph->side) (void)hipStreamDestroy(graph->side);
+  delete graph;
+  return DSA_OK;
+}
+
+// Internal (not in the public header): selects the fp8 MFMA form of the scan.
+int dsa_internal_set_scan_variant(int v) {
+  dsa::set_scan_variant(v);
+  return DSA_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,159 @@
+"""Paged decode layers and the MLI lag schedule on the GPU.
+
+:class:`DecodeLayer` owns the device buffers of one DSA decode layer for a
+batch of B requests (one decode row each): the indexer query/weights, the
+paged fp8 index-K cache, the fp8 latent KV pool, the attention query, the
+score slab, the selection and the attention output.  :class:`MLISchedule`
+runs a stack of layers under the Multi-layer Indexer lag -- layer i attends
+the selection of the last earlier indexing layer while layer i's own
+indexer runs on a second stream -- eagerly or as one captured hipGraph
+(C ABI ``dsa_mli_graph_*``).
+
+Reference: DSAModel.forward LAGGED_FUSED (model.py:109-136),
+DSALayer.fused_attention_and_indices (dsa_layer.py:173-192), the serving
+side-stream fork/join (sglang overlay patch P:1774-1833, P:2942-2997) and
+IndexCache reuse (P:1835-1904).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import LayerArgs
+from .ops import sparse_mla_workspace
+
+
+@dataclass
+class DecodeLayer:
+    """Device buffers of one decode layer (all contiguous, on one GPU)."""
+
+    q_fp8: torch.Tensor | None       # [B, Hidx, 128] uint8 (None: no indexer)
+    w: torch.Tensor | None           # [B, Hidx] f32, q-scale folded
+    index_k: torch.Tensor | None     # [P, 8448] uint8
+    q_bf16: torch.Tensor             # [B, H, 576] bf16
+    kv_pool: torch.Tensor            # [P*64, 656] uint8
+    page_table: torch.Tensor         # [B, pt_stride] int32
+    seq_lens: torch.Tensor           # [B] int32
+    slab_stride: int
+    topk: int = 2048
+    nsplit: int = 0
+    sm_scale: float = 576 ** -0.5
+
+    def __post_init__(self) -> None:
+        B = self.q_bf16.shape[0]
+        dev = self.q_bf16.device
+        self.scores = torch.empty(B, self.slab_stride, dtype=torch.float32, device=dev)
+        self.next_idx = torch.full((B, self.topk), -1, dtype=torch.int32, device=dev)
+        self.workspace = sparse_mla_workspace(B, self.q_bf16.shape[1], self.nsplit, dev)
+        self.out = torch.zeros(B, self.q_bf16.shape[1], 512, dtype=torch.bfloat16, device=dev)
+
+    @property
+    def has_indexer(self) -> bool:
+        return self.q_fp8 is not None
+
+    def args(self, attend_idx: torch.Tensor | None = None, indexer: bool = True,
+             attention: bool = True) -> LayerArgs:
+        """C-ABI argument block.  attend_idx=None: the schedule decides."""
+        a = LayerArgs()
+        B, H, _ = self.q_bf16.shape
+        if indexer and self.has_indexer:
+            a.q_fp8 = self.q_fp8.data_ptr()
+            a.w = self.w.data_ptr()
+            a.index_k = self.index_k.data_ptr()
+            a.num_idx_pages = self.index_k.shape[0]
+            a.Hidx = self.q_fp8.shape[1]
+        a.scores = self.scores.data_ptr()
+        a.next_idx = self.next_idx.data_ptr()
+        if attention:
+            a.q_bf16 = self.q_bf16.data_ptr()
+            a.kv_pool = self.kv_pool.data_ptr()
+            a.kv_rows = self.kv_pool.shape[0]
+            a.workspace = self.workspace.data_ptr()
+            a.out_bf16 = self.out.data_ptr()
+        a.attend_idx = None if attend_idx is None else attend_idx.data_ptr()
+        a.page_table = self.page_table.data_ptr()
+        a.seq_lens = self.seq_lens.data_ptr()
+        a.B = B
+        a.H = H
+        a.topk = self.topk
+        a.nsplit = self.nsplit
+        a.pt_stride = self.page_table.shape[1]
+        a.slab_stride = self.slab_stride
+        a.sm_scale = self.sm_scale
+        return a
+
+    def run(self, attend_idx: torch.Tensor | None = None) -> None:
+        """One layer on the current stream: indexer -> next_idx, attention
+        over attend_idx (lagged) or over next_idx (same-layer, baseline DSA)."""
+        a = self.args(attend_idx)
+        _lib.call("dsa_decode_layer", ctypes.byref(a), torch.cuda.current_stream().cuda_stream)
+
+
+def _arg_array(args: list[LayerArgs]):
+    arr = (LayerArgs * len(args))()
+    for i, a in enumerate(args):
+        arr[i] = a
+    return arr
+
+
+class MLISchedule:
+    """A stack of decode layers under the MLI lag.
+
+    ``first_attend`` is the selection layer 0 attends (the previous step's or
+    a cold-start set).  Layers whose indexer is disabled (IndexCache reuse)
+    attend the most recent earlier selection.
+    """
+
+    def __init__(self, layers: list[DecodeLayer], first_attend: torch.Tensor,
+                 indexer: bool = True, attention: bool = True,
+                 attend_all_first: bool = False) -> None:
+        """indexer/attention=False drop that half of every layer (timing of
+        the other half alone); attend_all_first makes every layer attend
+        ``first_attend`` (attention-only timing with the same gather volume)."""
+        self.layers = layers
+        self.first_attend = first_attend
+        self._args = []
+        for i, layer in enumerate(layers):
+            att = first_attend if (i == 0 or attend_all_first) else None
+            self._args.append(layer.args(att, indexer=indexer, attention=attention))
+        self._arr = _arg_array(self._args)
+        self._graph = None
+        self._side = None
+
+    def run_eager(self) -> None:
+        if self._side is None:
+            self._side = torch.cuda.Stream()
+        main = torch.cuda.current_stream()
+        # side-stream buffers are used across the fork: hold refs (allocator
+        # safety, as P:2986-2990 does) -- the layers own them for our lifetime
+        _lib.call("dsa_mli_run_eager", self._arr, len(self._args), main.cuda_stream,
+                  self._side.cuda_stream)
+
+    def capture(self) -> None:
+        """Capture the whole step into one hipGraph (two streams inside)."""
+        if self._graph is not None:
+            return
+        h = ctypes.c_void_p()
+        cap = torch.cuda.Stream()
+        _lib.call("dsa_mli_graph_create", self._arr, len(self._args), cap.cuda_stream, ctypes.byref(h))
+        self._graph = h
+
+    def replay(self) -> None:
+        if self._graph is None:
+            self.capture()
+        _lib.call("dsa_mli_graph_launch", self._graph, torch.cuda.current_stream().cuda_stream)
+
+    def close(self) -> None:
+        if self._graph is not None:
+            _lib.load().dsa_mli_graph_destroy(self._graph)
+            self._graph = None
+
+    def __del__(self) -> None:
+        try:
+            self.close()
+        except Exception:
+            pass

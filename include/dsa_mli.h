@@ -1,0 +1,193 @@
+/*
+ * dsa_mli.h — C ABI of libdsa_mli.so, the MI355X (gfx950) DeepSeek Sparse
+ * Attention decode hot path: lightning-indexer scan over a paged fp8 key
+ * cache, exact top-k select, split-K sparse MLA over the fp8 656-byte latent
+ * pool, and the Multi-layer Indexer (MLI) lag schedule as one captured
+ * two-stream hipGraph.
+ *
+ * Conventions (every entry point):
+ *   - plain device pointers and sizes; no torch types;
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream);
+ *   - the call only enqueues work; it never allocates device memory and
+ *     never synchronises; caller owns every output and scratch buffer;
+ *   - return 0 (DSA_OK) on success, a negative DSA_ERR_* code when an
+ *     argument violates the contract (nothing is launched then), and
+ *     DSA_ERR_HIP when the HIP launch itself failed;
+ *     dsa_last_error() returns a message for the calling thread;
+ *   - per-row context lengths are read from device memory (`seq_lens`), so a
+ *     captured launch replays correctly as contexts grow.
+ *
+ * Data layouts in HBM (shared by all entry points):
+ *   index-K page  : 8448 bytes = [64 keys x 128 B e4m3][64 x fp32 key scale]
+ *                   token g of row b lives in page page_table[b*pt_stride + g/64],
+ *                   slot g%64.
+ *   latent KV row : 656 bytes = [512 e4m3][4 fp32 scales, one per 128 dims]
+ *                   [64 bf16 rope]; the row of token g of row b is KV slot
+ *                   page_table[b*pt_stride + g/64]*64 + g%64.
+ *   e4m3          : OCP float8 e4m3fn (bias 7, max 448, 0x7f/0xff = NaN).
+ */
+#ifndef DSA_MLI_H
+#define DSA_MLI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DSA_OK 0
+#define DSA_ERR_INVALID_ARG (-1)  /* null pointer, bad size or stride */
+#define DSA_ERR_UNSUPPORTED (-2)  /* shape outside the compiled kernels */
+#define DSA_ERR_HIP (-3)          /* hipLaunch / hipGraph call failed */
+
+#define DSA_PAGE_TOKENS 64
+#define DSA_INDEX_DIM 128
+#define DSA_INDEX_PAGE_BYTES 8448 /* 64*128 + 64*4 */
+#define DSA_LATENT_DIM 512
+#define DSA_ROPE_DIM 64
+#define DSA_QK_DIM 576
+#define DSA_LATENT_ROW_BYTES 656  /* 512 + 4*4 + 64*2 */
+#define DSA_TOPK_MAX_CTX 262144   /* longest row the top-k select accepts */
+
+/* dsa_topk flags */
+#define DSA_TOPK_POSITION_ORDER 0 /* selected indices ascending, pads last */
+#define DSA_TOPK_SORTED 1         /* score descending, ties lower index first */
+
+/* Message for the last failing call on this host thread ("" if none). */
+const char* dsa_last_error(void);
+
+/* Library version string. */
+const char* dsa_version(void);
+
+/*
+ * (1) Lightning-indexer scan.
+ *   scores[b, g] = kscale[g] * sum_h w[b,h] * ReLU( sum_d q[b,h,d] * k[g,d] )
+ * for g < seq_lens[b]; scores[b, g] = -inf for seq_lens[b] <= g < slab_stride.
+ *   q_fp8      [B, Hidx, 128] e4m3 (the per-head query scale is folded into w)
+ *   w          [B, Hidx] fp32
+ *   index_k    [num_pages, 8448] bytes
+ *   page_table [B, pt_stride] int32 physical page ids (ids outside
+ *              [0, num_pages) score -inf instead of being read)
+ *   seq_lens   [B] int32 (clamped to min(pt_stride*64, slab_stride))
+ *   scores     [B, slab_stride] fp32
+ * Hidx must be 16, 32, 48 or 64.
+ * Replaces: reference kernels/cuda_fused_sparse_splitk.py hp_indexer_block
+ * (K:1677-2157) reached through launch_fused_sparse_splitk_paged
+ * (K:2770) with with_select=1, and ref_indexer_logits_fp8 (K:2990-2992);
+ * CPU semantics attention_core.py:27-49 (indexer_logits).
+ */
+int dsa_indexer_scan(const void* q_fp8, const float* w, const void* index_k,
+                     int64_t num_pages, const int32_t* page_table,
+                     const int32_t* seq_lens, float* scores, int B, int Hidx,
+                     int pt_stride, int slab_stride, void* stream);
+
+/*
+ * (2) Exact top-k select over each row's first seq_lens[b] scores.
+ * Order of selection: score descending, ties -> lower index first; NaN
+ * ranks above +inf and -0.0 equals +0.0.  Selected entries whose score is
+ * not finite become `pad_value`, as do the slots beyond seq_lens[b] when the
+ * row is shorter than topk.
+ *   flags = DSA_TOPK_POSITION_ORDER: out[b] = selected finite indices in
+ *           ascending index order, then pads;
+ *   flags = DSA_TOPK_SORTED: out[b] in selection order (torch.topk order
+ *           with the lower-index tie rule), non-finite entries -> pad in place.
+ * page_table != NULL: each emitted position g is replaced by its KV slot
+ * page_table[b*pt_stride + g/64]*64 + g%64 (position order only).
+ *   scores  [B, slab_stride] fp32;  out_idx [B, topk] int32
+ * Requires topk <= 8192 (<= 4096 with DSA_TOPK_SORTED) and
+ * slab_stride <= DSA_TOPK_MAX_CTX.
+ * Replaces: reference attention_core.py:66-91 (select_topk), and on the GPU
+ * tl_topk (tilelang_dsa/topk_selector.py:355-386) and the in-kernel exact
+ * select with hp_page_to_slot (K:1097-1144, K:1248-1310).
+ */
+int dsa_topk(const float* scores, const int32_t* seq_lens,
+             const int32_t* page_table, int pt_stride, int32_t* out_idx, int B,
+             int slab_stride, int topk, int flags, int32_t pad_value,
+             void* stream);
+
+/*
+ * (3) Split-K sparse MLA decode over the fp8 latent pool.
+ *   out[b,h,:] = sum_j softmax_j(sm_scale * q[b,h,:] . kv_j) * kv_j[:512]
+ * over the j in idx[b, :topk] with 0 <= idx < kv_rows (others are masked);
+ * kv_j = dequant(row idx[b,j]) = bf16_rn(f32(e4m3) * scale[d/128]) for d<512,
+ * rope bf16 for d>=512.  A row with no valid index gives 0.
+ *   q        [B, H, 576] bf16;     kv_pool [kv_rows, 656] bytes
+ *   idx      [B, topk] int32 KV slots
+ *   part_o   workspace, dsa_sparse_mla_workspace_bytes() bytes
+ *   out      [B, H, 512] bf16
+ * H must be a multiple of 16; 1 <= nsplit <= 128 (nsplit=0: automatic).
+ * Replaces: hp_attention_block + combine (K:1312-1666, K:996-1045) and
+ * ref_sparse_mla (K:2950-2966); CPU semantics attention_core.py:94-146.
+ */
+size_t dsa_sparse_mla_workspace_bytes(int B, int H, int nsplit);
+int dsa_sparse_mla_decode(const void* q_bf16, const void* kv_pool,
+                          int64_t kv_rows, const int32_t* idx, void* workspace,
+                          void* out_bf16, int B, int H, int topk, int nsplit,
+                          float sm_scale, void* stream);
+
+/*
+ * (4) One DSA decode layer on one stream:
+ *   scan -> top-k (position order, KV-slot output into next_idx) and
+ *   attention over attend_idx (the lagged set), or over this layer's own
+ *   fresh selection when attend_idx == NULL (baseline DSA).
+ * scores [B, slab_stride] fp32 scratch; next_idx [B, topk] int32.
+ * Replaces: DSALayer.fused_attention_and_indices (dsa_layer.py:173-192)
+ * for one decode row per request.
+ */
+typedef struct dsa_layer_args {
+  /* indexer operands (NULL q_fp8: this layer runs no indexer) */
+  const void* q_fp8;        /* [B, Hidx, 128] e4m3 */
+  const float* w;           /* [B, Hidx] */
+  const void* index_k;      /* [num_idx_pages, 8448] */
+  int64_t num_idx_pages;
+  float* scores;            /* [B, slab_stride] scratch */
+  int32_t* next_idx;        /* [B, topk] out: KV slots, -1 pad */
+  /* attention operands */
+  const void* q_bf16;       /* [B, H, 576] */
+  const void* kv_pool;      /* [kv_rows, 656] */
+  int64_t kv_rows;
+  const int32_t* attend_idx;/* [B, topk] KV slots; NULL = next_idx */
+  void* workspace;          /* dsa_sparse_mla_workspace_bytes(B,H,nsplit) */
+  void* out_bf16;           /* [B, H, 512] */
+  /* shared */
+  const int32_t* page_table;/* [B, pt_stride] */
+  const int32_t* seq_lens;  /* [B] */
+  int B, Hidx, H, topk, nsplit, pt_stride, slab_stride;
+  float sm_scale;
+} dsa_layer_args;
+
+int dsa_decode_layer(const dsa_layer_args* args, void* stream);
+
+/*
+ * (5) MLI lag schedule as one hipGraph.  Layer i's attention runs on the
+ * main stream over the set it is given; layer i's indexer (scan + top-k)
+ * runs concurrently on a second stream and its selection is joined at the
+ * entry of layer i+1's attention.  Layer i+1's indexer waits for layer i's
+ * attention (its query derives from layer i+1's input).  attend_idx of a
+ * layer that is NULL means "the selection produced most recently by an
+ * earlier layer of the graph" (IndexCache reuse + lag); the first layer
+ * must be given an explicit attend_idx.  A layer whose q_fp8 is NULL runs
+ * no indexer.
+ * Replaces: DSAModel.forward LAGGED_FUSED (model.py:109-136) and the serving
+ * side-stream fork/join (sglang overlay patch P:1774-1833, P:2942-2997).
+ */
+typedef struct dsa_mli_graph dsa_mli_graph;
+int dsa_mli_graph_create(const dsa_layer_args* layers, int num_layers,
+                         void* capture_stream, dsa_mli_graph** out_graph);
+int dsa_mli_graph_launch(dsa_mli_graph* graph, void* stream);
+int dsa_mli_graph_destroy(dsa_mli_graph* graph);
+
+/*
+ * Same schedule as dsa_mli_graph, enqueued eagerly (no graph): attention on
+ * `stream`, indexers on `side_stream` (a different stream of the same
+ * device), with event fork/join between them.  Returns once enqueued.
+ */
+int dsa_mli_run_eager(const dsa_layer_args* layers, int num_layers,
+                      void* stream, void* side_stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSA_MLI_H */

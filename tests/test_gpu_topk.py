@@ -1,0 +1,120 @@
+"""GPU parity: exact top-k select (dsa_topk) vs the oracle, bit-exact.
+
+Given identical fp32 scores the selected indices must be identical, with
+the lower index winning ties (the path's bar for index work).  Cases cover
+the reference's select contract (attention_core.py:66-91): rows shorter
+than k (sentinel/pad), non-finite scores, forced ties at the threshold,
+all-equal rows (the threshold bin overflows the on-chip candidate buffer),
+-0.0/+0.0, and the longest supported rows.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import dsa_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _gpu_topk(scores, lens, k, sorted_, pad=-1, pt=None, dev="cuda"):
+    from lagged_indexer_dsa_amd import ops
+
+    s = torch.from_numpy(np.ascontiguousarray(scores, dtype=np.float32)).to(dev)
+    l = torch.from_numpy(np.asarray(lens, dtype=np.int32)).to(dev)
+    p = None if pt is None else torch.from_numpy(pt).to(dev)
+    out = ops.topk(s, l, k, sorted=sorted_, pad_value=pad, page_table=p)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def _check(scores, lens, k, sorted_, dev, pad=-1, pt=None):
+    got = _gpu_topk(scores, lens, k, sorted_, pad, pt, dev)
+    ref = O.topk_select(scores, np.asarray(lens), k, sorted_=sorted_, pad=pad, page_table=pt)
+    bad = np.nonzero((got != ref).any(axis=1))[0]
+    assert bad.size == 0, f"rows {bad[:5]} differ (first: got {got[bad[0]][:8]} ref {ref[bad[0]][:8]})"
+
+
+@pytest.mark.parametrize("sorted_", [False, True])
+def test_topk_random_ragged(dev, sorted_):
+    rng = np.random.default_rng(1)
+    lens = [8192, 2048, 2047, 100, 0, 1, 5000, 3000]
+    print(f"[topk] random ragged sorted={sorted_}", flush=True)
+    s = rng.standard_normal((len(lens), 8192)).astype(np.float32)
+    _check(s, lens, 2048, sorted_, dev)
+
+
+@pytest.mark.parametrize("sorted_", [False, True])
+def test_topk_forced_ties(dev, sorted_):
+    rng = np.random.default_rng(2)
+    print(f"[topk] forced ties sorted={sorted_}", flush=True)
+    # few distinct values: thousands of ties straddle the threshold
+    s = rng.integers(-20, 20, (4, 20000)).astype(np.float32) * 0.25
+    s[1] = np.round(rng.standard_normal(20000) * 8) / 8
+    s[2, ::3] = -0.0
+    s[2, 1::3] = 0.0
+    _check(s, [20000, 19999, 20000, 7000], 2048, sorted_, dev)
+
+
+@pytest.mark.parametrize("sorted_", [False, True])
+def test_topk_all_equal_rows_overflow_path(dev, sorted_):
+    print(f"[topk] all equal sorted={sorted_}", flush=True)
+    s = np.full((3, 50000), 1.5, dtype=np.float32)
+    s[1] = 0.0
+    s[2, :] = 2.0
+    s[2, 40000:] = 3.0   # 10000 above, the rest tied
+    _check(s, [50000, 50000, 50000], 2048, sorted_, dev)
+
+
+@pytest.mark.parametrize("sorted_", [False, True])
+def test_topk_nonfinite(dev, sorted_):
+    rng = np.random.default_rng(3)
+    print(f"[topk] non-finite sorted={sorted_}", flush=True)
+    s = rng.standard_normal((4, 6000)).astype(np.float32)
+    s[0, rng.integers(0, 6000, 50)] = np.inf
+    s[0, rng.integers(0, 6000, 50)] = np.nan
+    s[1, 1000:] = -np.inf                   # fewer finite than k -> pads
+    s[2, :] = -np.inf
+    s[3, rng.integers(0, 6000, 3000)] = -np.inf
+    _check(s, [6000] * 4, 2048, sorted_, dev, pad=6000)
+
+
+def test_topk_page_slot_mapping(dev):
+    rng = np.random.default_rng(4)
+    print("[topk] slot mapping", flush=True)
+    lens = [9000, 70000]
+    s = rng.standard_normal((2, 70016)).astype(np.float32)
+    pt = np.stack([rng.permutation(5000)[:1094] for _ in range(2)]).astype(np.int32)
+    _check(s, lens, 2048, False, dev, pt=pt)
+
+
+@pytest.mark.parametrize("k", [1, 7, 2048, 4096])
+def test_topk_sizes_sorted(dev, k):
+    rng = np.random.default_rng(5 + k)
+    print(f"[topk] k={k}", flush=True)
+    s = rng.standard_normal((2, 30000)).astype(np.float32)
+    _check(s, [30000, 4000], k, True, dev)
+    _check(s, [30000, 4000], k, False, dev)
+
+
+@pytest.mark.parametrize("ctx", [131072, 196608, 262144])
+def test_topk_max_sizes(dev, ctx):
+    rng = np.random.default_rng(ctx)
+    print(f"[topk] ctx={ctx}", flush=True)
+    s = rng.standard_normal((2, ctx)).astype(np.float32)
+    _check(s, [ctx, ctx - 5], 2048, False, dev)
+    _check(s, [ctx, ctx - 5], 2048, True, dev)
+
+
+def test_topk_rejects_bad_args(dev):
+    from lagged_indexer_dsa_amd import ops
+    from lagged_indexer_dsa_amd._lib import DsaError
+
+    s = torch.zeros(1, 100, device=dev)
+    l = torch.full((1,), 100, dtype=torch.int32, device=dev)
+    with pytest.raises(DsaError):
+        ops.topk(s, l, 5000, sorted=True)
+    with pytest.raises(DsaError):
+        ops.topk(s, l, 0)
