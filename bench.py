@@ -64,7 +64,7 @@ def time_graph(fn, iters: int, torch) -> float:
 
 def event_ms(fn, iters: int, torch) -> float:
     """Average per-launch device time of fn() with HIP events recorded on the
-    stream fn launches on (torch's current stream)."""
+    stream fn launches on (torch's current stream), one event pair per launch."""
     pairs = []
     for _ in range(iters):
         a = torch.cuda.Event(enable_timing=True)
@@ -75,6 +75,29 @@ def event_ms(fn, iters: int, torch) -> float:
         pairs.append((a, b))
     torch.cuda.synchronize()
     return statistics.mean(a.elapsed_time(b) for a, b in pairs)
+
+
+def graph_event_ms(fn, iters: int, torch) -> float:
+    """Per-launch time of fn() from HIP events around one replay of a graph
+    holding `iters` back-to-back launches (captured on torch's current
+    stream, so the events bracket exactly those kernels)."""
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for _ in range(iters):
+                fn()
+    torch.cuda.current_stream().wait_stream(s)
+    g.replay()
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / iters
 
 
 def cpu_baseline(ctx: int, budget_s: float = 15.0) -> dict:
@@ -163,15 +186,16 @@ def main() -> int:
                                     L0.slab_stride, out=L0.scores)
     for _ in range(10):
         scan()
-    scan_ms = event_ms(scan, 200, torch)
+    scan_ms = graph_event_ms(scan, 100, torch)
+    scan_ms_pairs = event_ms(scan, 100, torch)
     sb = scan_bytes(lens)
     scan_gbs = sb / (scan_ms * 1e-3) / 1e9
     topk_fn = lambda: ops.topk(L0.scores, L0.seq_lens, 2048, page_table=L0.page_table,
-                               out=L0.next_idx)
-    topk_ms = event_ms(topk_fn, 100, torch)
+                               out=L0.next_idx, scratch=L0.topk_scratch)
+    topk_ms = graph_event_ms(topk_fn, 50, torch)
     attn_fn = lambda: ops.sparse_mla_decode(L0.q_bf16, L0.kv_pool, first, workspace=L0.workspace,
                                             out=L0.out)
-    attn_ms = event_ms(attn_fn, 100, torch)
+    attn_ms = graph_event_ms(attn_fn, 50, torch)
     ab = attn_bytes(B)
 
     us_layer = ms_step * 1e3 / n_layers
@@ -196,7 +220,8 @@ def main() -> int:
         "tokens_per_s": round(B / (us_layer * 1e-6), 1),
         "indexer_scan_GBps": round(scan_gbs, 1),
         "kernel_us": {"indexer_scan": round(scan_ms * 1e3, 3), "topk": round(topk_ms * 1e3, 3),
-                      "sparse_mla+combine": round(attn_ms * 1e3, 3)},
+                      "sparse_mla+combine": round(attn_ms * 1e3, 3),
+                      "indexer_scan_event_pairs": round(scan_ms_pairs * 1e3, 3)},
         "attention_gather_GBps": round(ab / (attn_ms * 1e-3) / 1e9, 1),
         "mli": {"graph_ms": round(t_full, 5), "attn_only_ms": round(t_attn, 5),
                 "indexer_only_ms": round(t_idx, 5),

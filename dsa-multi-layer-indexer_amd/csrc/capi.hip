@@ -18,8 +18,9 @@ hipError_t launch_indexer_scan(const uint8_t* q8, const float* w, const uint8_t*
                                int B, int Hidx, int pt_stride, int slab_stride, hipStream_t s);
 void set_scan_variant(int v);
 hipError_t launch_topk(const float* scores, const int* seq_lens, const int* page_table,
-                       int pt_stride, int* out, int B, int slab_stride, int K, int sorted,
+                       int pt_stride, void* scratch, int* out, int B, int slab, int K, int sorted,
                        int pad, hipStream_t s);
+size_t topk_scratch_bytes(int B, int slab);
 hipError_t launch_sparse_mla(const uint16_t* q, const uint8_t* pool, long kv_rows,
                              const int* idx, void* workspace, uint16_t* out, int B, int H,
                              int topk, int nsplit, float sm_scale, hipStream_t s);
@@ -67,9 +68,12 @@ int check_scan(const void* q_fp8, const float* w, const void* index_k, int64_t n
 }
 
 int check_topk(const float* scores, const int32_t* seq_lens, const int32_t* page_table,
-               int pt_stride, const int32_t* out_idx, int B, int slab_stride, int topk,
-               int flags) {
-  DSA_REQUIRE(scores && seq_lens && out_idx, DSA_ERR_INVALID_ARG, "dsa_topk: null pointer argument");
+               int pt_stride, const void* scratch, const int32_t* out_idx, int B,
+               int slab_stride, int topk, int flags) {
+  DSA_REQUIRE(scores && seq_lens && out_idx && scratch, DSA_ERR_INVALID_ARG,
+              "dsa_topk: null pointer argument");
+  DSA_REQUIRE(((uintptr_t)scratch & 15) == 0, DSA_ERR_INVALID_ARG,
+              "dsa_topk: scratch must be 16-byte aligned");
   DSA_REQUIRE(B >= 1, DSA_ERR_INVALID_ARG, "dsa_topk: B must be >= 1 (got %d)", B);
   DSA_REQUIRE(topk >= 1, DSA_ERR_INVALID_ARG, "dsa_topk: topk must be >= 1 (got %d)", topk);
   DSA_REQUIRE(flags == DSA_TOPK_POSITION_ORDER || flags == DSA_TOPK_SORTED, DSA_ERR_INVALID_ARG,
@@ -86,8 +90,9 @@ int check_topk(const float* scores, const int32_t* seq_lens, const int32_t* page
 }
 
 int check_mla(const void* q_bf16, const void* kv_pool, int64_t kv_rows, const int32_t* idx,
-              const void* workspace, const void* out_bf16, int B, int H, int topk, int nsplit) {
-  DSA_REQUIRE(q_bf16 && kv_pool && idx && workspace && out_bf16, DSA_ERR_INVALID_ARG,
+              const void* workspace, const void* out_bf16, int B, int H, int topk, int nsplit,
+              bool idx_required = true) {
+  DSA_REQUIRE(q_bf16 && kv_pool && (idx || !idx_required) && workspace && out_bf16, DSA_ERR_INVALID_ARG,
               "dsa_sparse_mla_decode: null pointer argument");
   DSA_REQUIRE(B >= 1 && B <= 65535, DSA_ERR_INVALID_ARG, "dsa_sparse_mla_decode: bad B %d", B);
   DSA_REQUIRE(H >= 16 && H % 16 == 0 && H <= 16 * 64, DSA_ERR_UNSUPPORTED,
@@ -106,23 +111,25 @@ int resolve_nsplit(int nsplit, int topk) {
   return nsplit > 0 ? nsplit : dsa::sparse_mla_auto_nsplit(topk);
 }
 
-int check_layer(const dsa_layer_args* a) {
+// in_schedule: attend_idx == NULL is resolved by the MLI schedule (the most
+// recent earlier selection) instead of meaning "this layer's own selection".
+int check_layer(const dsa_layer_args* a, bool in_schedule = false) {
   DSA_REQUIRE(a != nullptr, DSA_ERR_INVALID_ARG, "dsa_layer_args is null");
   int rc;
   if (a->q_fp8) {
     rc = check_scan(a->q_fp8, a->w, a->index_k, a->num_idx_pages, a->page_table, a->seq_lens,
                     a->scores, a->B, a->Hidx, a->pt_stride, a->slab_stride);
     if (rc) return rc;
-    rc = check_topk(a->scores, a->seq_lens, a->page_table, a->pt_stride, a->next_idx, a->B,
-                    a->slab_stride, a->topk, DSA_TOPK_POSITION_ORDER);
+    rc = check_topk(a->scores, a->seq_lens, a->page_table, a->pt_stride, a->topk_scratch,
+                    a->next_idx, a->B, a->slab_stride, a->topk, DSA_TOPK_POSITION_ORDER);
     if (rc) return rc;
   }
   if (a->q_bf16) {
     const int32_t* att = a->attend_idx ? a->attend_idx : a->next_idx;
-    DSA_REQUIRE(a->attend_idx || a->q_fp8, DSA_ERR_INVALID_ARG,
+    DSA_REQUIRE(in_schedule || a->attend_idx || a->q_fp8, DSA_ERR_INVALID_ARG,
                 "dsa_decode_layer: attention needs attend_idx or an indexer");
     rc = check_mla(a->q_bf16, a->kv_pool, a->kv_rows, att, a->workspace, a->out_bf16, a->B, a->H,
-                   a->topk, a->nsplit);
+                   a->topk, a->nsplit, /*idx_required=*/!in_schedule);
     if (rc) return rc;
   }
   return DSA_OK;
@@ -136,7 +143,8 @@ int enqueue_indexer(const dsa_layer_args* a, hipStream_t s) {
       "indexer scan launch");
   if (rc) return rc;
   return hip_status(dsa::launch_topk(a->scores, a->seq_lens, a->page_table, a->pt_stride,
-                                     a->next_idx, a->B, a->slab_stride, a->topk, 0, -1, s),
+                                     a->topk_scratch, a->next_idx, a->B, a->slab_stride, a->topk,
+                                     0, -1, s),
                     "top-k launch");
 }
 
@@ -220,12 +228,18 @@ int dsa_indexer_scan(const void* q_fp8, const float* w, const void* index_k, int
                     "indexer scan launch");
 }
 
+size_t dsa_topk_scratch_bytes(int B, int slab_stride) {
+  if (B < 1 || slab_stride < 1 || slab_stride > DSA_TOPK_MAX_CTX) return 0;
+  return dsa::topk_scratch_bytes(B, slab_stride);
+}
+
 int dsa_topk(const float* scores, const int32_t* seq_lens, const int32_t* page_table,
-             int pt_stride, int32_t* out_idx, int B, int slab_stride, int topk, int flags,
-             int32_t pad_value, void* stream) {
-  int rc = check_topk(scores, seq_lens, page_table, pt_stride, out_idx, B, slab_stride, topk, flags);
+             int pt_stride, void* scratch, int32_t* out_idx, int B, int slab_stride, int topk,
+             int flags, int32_t pad_value, void* stream) {
+  int rc = check_topk(scores, seq_lens, page_table, pt_stride, scratch, out_idx, B, slab_stride,
+                      topk, flags);
   if (rc) return rc;
-  return hip_status(dsa::launch_topk(scores, seq_lens, page_table, pt_stride, out_idx, B,
+  return hip_status(dsa::launch_topk(scores, seq_lens, page_table, pt_stride, scratch, out_idx, B,
                                      slab_stride, topk, flags == DSA_TOPK_SORTED, pad_value,
                                      (hipStream_t)stream),
                     "top-k launch");
@@ -262,7 +276,7 @@ static int check_mli(const dsa_layer_args* layers, int n) {
   DSA_REQUIRE(layers && n >= 1, DSA_ERR_INVALID_ARG, "mli: need at least one layer");
   const int32_t* carried = nullptr;
   for (int i = 0; i < n; ++i) {
-    int rc = check_layer(&layers[i]);
+    int rc = check_layer(&layers[i], true);
     if (rc) return rc;
     if (layers[i].q_bf16 && !layers[i].attend_idx && !carried)
       return fail(DSA_ERR_INVALID_ARG, "mli layer %d: attend_idx is NULL and no earlier layer indexes", i);

@@ -218,53 +218,54 @@ __global__ __launch_bounds__(kAttnThreads) void sparse_mla_split_kernel(
   }
 }
 
-constexpr int kCombThreads = 256;
+constexpr int kCombCols = 16;                               // output dims per block
+constexpr int kCombThreads = kHeadsPerGroup * kCombCols / 4;  // one float4 per thread
 constexpr int kMaxSplit = 128;
 
 // Log-sum-exp merge of the split partials (reference combine_kernel
 // K:996-1045): m* = max m_s, L = sum l_s 2^(m_s-m*), out = sum O_s 2^(m_s-m*) / L.
 // Splits with m = -inf contribute nothing; a row with no valid key gives 0.
+// Block (column slice, head group, row): 16 heads x 16 dims, so the merge
+// of a b=1 row spreads over 32 workgroups.
 __global__ __launch_bounds__(kCombThreads) void sparse_mla_combine_kernel(
     const float* __restrict__ part_o, const float* __restrict__ part_ml,
     uint16_t* __restrict__ out, int H, int nsplit) {
   __shared__ float wgt[kMaxSplit * kHeadsPerGroup];
-  const int hg = blockIdx.x, b = blockIdx.y, nhg = gridDim.x;
+  const int cb = blockIdx.x, hg = blockIdx.y, b = blockIdx.z, nhg = gridDim.y;
   const int t = threadIdx.x;
   const long pblk0 = ((long)b * nhg + hg) * nsplit;
   if (t < kHeadsPerGroup) {
+    const float* ml = part_ml + pblk0 * 2 * kHeadsPerGroup + 2 * t;
     float mx = -INFINITY;
-    for (int sp = 0; sp < nsplit; ++sp) mx = fmaxf(mx, part_ml[(pblk0 + sp) * 2 * kHeadsPerGroup + 2 * t]);
+    for (int sp = 0; sp < nsplit; ++sp) mx = fmaxf(mx, ml[sp * 2 * kHeadsPerGroup]);
     float L = 0.f;
     if (mx != -INFINITY)
       for (int sp = 0; sp < nsplit; ++sp) {
-        const float ms = part_ml[(pblk0 + sp) * 2 * kHeadsPerGroup + 2 * t];
-        if (ms != -INFINITY) L += part_ml[(pblk0 + sp) * 2 * kHeadsPerGroup + 2 * t + 1] * exp2f(ms - mx);
+        const float ms = ml[sp * 2 * kHeadsPerGroup];
+        if (ms != -INFINITY) L += ml[sp * 2 * kHeadsPerGroup + 1] * exp2f(ms - mx);
       }
     const float inv = (mx != -INFINITY && L > 0.f) ? 1.f / L : 0.f;
     for (int sp = 0; sp < nsplit; ++sp) {
-      const float ms = part_ml[(pblk0 + sp) * 2 * kHeadsPerGroup + 2 * t];
+      const float ms = ml[sp * 2 * kHeadsPerGroup];
       wgt[sp * kHeadsPerGroup + t] = (ms != -INFINITY) ? exp2f(ms - mx) * inv : 0.f;
     }
   }
   __syncthreads();
-  // 16 heads x 512 dims as float4: 2048 vectors, 8 per thread
-  for (int v = t; v < kHeadsPerGroup * DSA_LATENT_DIM / 4; v += kCombThreads) {
-    const int h = v / (DSA_LATENT_DIM / 4);
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int sp = 0; sp < nsplit; ++sp) {
-      const float wt = wgt[sp * kHeadsPerGroup + h];
-      if (wt != 0.f) {
-        const float4 x = reinterpret_cast<const float4*>(
-            part_o + (pblk0 + sp) * (kHeadsPerGroup * DSA_LATENT_DIM))[v];
-        acc.x += x.x * wt; acc.y += x.y * wt; acc.z += x.z * wt; acc.w += x.w * wt;
-      }
+  const int h = t / (kCombCols / 4);
+  const int d = cb * kCombCols + (t % (kCombCols / 4)) * 4;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  const float* po = part_o + pblk0 * (kHeadsPerGroup * DSA_LATENT_DIM) + h * DSA_LATENT_DIM + d;
+  for (int sp = 0; sp < nsplit; ++sp) {
+    const float wt = wgt[sp * kHeadsPerGroup + h];
+    if (wt != 0.f) {
+      const float4 x = *reinterpret_cast<const float4*>(po + (long)sp * (kHeadsPerGroup * DSA_LATENT_DIM));
+      acc.x += x.x * wt; acc.y += x.y * wt; acc.z += x.z * wt; acc.w += x.w * wt;
     }
-    uint2 pk;
-    pk.x = pack_bf16x2(acc.x, acc.y);
-    pk.y = pack_bf16x2(acc.z, acc.w);
-    const int d = (v % (DSA_LATENT_DIM / 4)) * 4;
-    *reinterpret_cast<uint2*>(out + ((long)b * H + hg * kHeadsPerGroup + h) * DSA_LATENT_DIM + d) = pk;
   }
+  uint2 pk;
+  pk.x = pack_bf16x2(acc.x, acc.y);
+  pk.y = pack_bf16x2(acc.z, acc.w);
+  *reinterpret_cast<uint2*>(out + ((long)b * H + hg * kHeadsPerGroup + h) * DSA_LATENT_DIM + d) = pk;
 }
 
 int sparse_mla_auto_nsplit(int topk) {
@@ -287,8 +288,8 @@ hipError_t launch_sparse_mla(const uint16_t* q, const uint8_t* pool, long kv_row
                      pool, kv_rows, idx, part_o, part_ml, H, topk, nsplit, sm_log2);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(sparse_mla_combine_kernel, dim3(nhg, B), dim3(kCombThreads), 0, s, part_o,
-                     part_ml, out, H, nsplit);
+  hipLaunchKernelGGL(sparse_mla_combine_kernel, dim3(DSA_LATENT_DIM / kCombCols, nhg, B),
+                     dim3(kCombThreads), 0, s, part_o, part_ml, out, H, nsplit);
   return hipGetLastError();
 }
 

@@ -50,7 +50,7 @@ class LayerArgs(ctypes.Structure):
 
     _fields_ = [
         ("q_fp8", _vp), ("w", _vp), ("index_k", _vp), ("num_idx_pages", _i64),
-        ("scores", _vp), ("next_idx", _vp),
+        ("scores", _vp), ("topk_scratch", _vp), ("next_idx", _vp),
         ("q_bf16", _vp), ("kv_pool", _vp), ("kv_rows", _i64), ("attend_idx", _vp),
         ("workspace", _vp), ("out_bf16", _vp),
         ("page_table", _vp), ("seq_lens", _vp),
@@ -67,7 +67,8 @@ SIGNATURES = {
     "dsa_last_error": (ctypes.c_char_p, []),
     "dsa_version": (ctypes.c_char_p, []),
     "dsa_indexer_scan": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp]),
-    "dsa_topk": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
+    "dsa_topk_scratch_bytes": (ctypes.c_size_t, [_i32, _i32]),
+    "dsa_topk": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
     "dsa_sparse_mla_workspace_bytes": (ctypes.c_size_t, [_i32, _i32, _i32]),
     "dsa_sparse_mla_decode": (_i32, [_vp, _vp, _i64, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _vp]),
     "dsa_decode_layer": (_i32, [ctypes.POINTER(LayerArgs), _vp]),

@@ -24,7 +24,7 @@ import torch
 
 from . import _lib
 from ._lib import LayerArgs
-from .ops import sparse_mla_workspace
+from .ops import sparse_mla_workspace, topk_scratch
 
 
 @dataclass
@@ -47,6 +47,7 @@ class DecodeLayer:
         B = self.q_bf16.shape[0]
         dev = self.q_bf16.device
         self.scores = torch.empty(B, self.slab_stride, dtype=torch.float32, device=dev)
+        self.topk_scratch = topk_scratch(B, self.slab_stride, dev)
         self.next_idx = torch.full((B, self.topk), -1, dtype=torch.int32, device=dev)
         self.workspace = sparse_mla_workspace(B, self.q_bf16.shape[1], self.nsplit, dev)
         self.out = torch.zeros(B, self.q_bf16.shape[1], 512, dtype=torch.bfloat16, device=dev)
@@ -67,6 +68,7 @@ class DecodeLayer:
             a.num_idx_pages = self.index_k.shape[0]
             a.Hidx = self.q_fp8.shape[1]
         a.scores = self.scores.data_ptr()
+        a.topk_scratch = self.topk_scratch.data_ptr()
         a.next_idx = self.next_idx.data_ptr()
         if attention:
             a.q_bf16 = self.q_bf16.data_ptr()

@@ -71,9 +71,17 @@ def indexer_scan(q_fp8: torch.Tensor, w: torch.Tensor, index_k: torch.Tensor,
     return out
 
 
+def topk_scratch(B: int, slab: int, device) -> torch.Tensor:
+    """Zero-filled scratch for :func:`topk` (each call leaves it zeroed)."""
+    nbytes = _lib.load().dsa_topk_scratch_bytes(B, slab)
+    if nbytes == 0:
+        raise RuntimeError(f"bad top-k scratch shape B={B} slab={slab}")
+    return torch.zeros(nbytes // 4, dtype=torch.int32, device=device)
+
+
 def topk(scores: torch.Tensor, seq_lens: torch.Tensor, k: int, sorted: bool = False,
          pad_value: int = -1, page_table: torch.Tensor | None = None,
-         out: torch.Tensor | None = None) -> torch.Tensor:
+         out: torch.Tensor | None = None, scratch: torch.Tensor | None = None) -> torch.Tensor:
     """Exact top-k per row (score desc, ties -> lower index), int32 [B, k].
 
     sorted=False: ascending positions (or KV slots through page_table), pads
@@ -91,9 +99,12 @@ def topk(scores: torch.Tensor, seq_lens: torch.Tensor, k: int, sorted: bool = Fa
         _dev(page_table)
     if out is None:
         out = torch.empty(B, k, dtype=torch.int32, device=scores.device)
-    _dev(out)
+    if scratch is None:
+        scratch = topk_scratch(B, slab, scores.device)
+    _dev(out, scratch)
     _lib.call("dsa_topk", scores.data_ptr(), seq_lens.data_ptr(), _ptr(page_table),
-              0 if page_table is None else page_table.shape[1], out.data_ptr(), B, slab, k,
+              0 if page_table is None else page_table.shape[1], scratch.data_ptr(),
+              out.data_ptr(), B, slab, k,
               DSA_TOPK_SORTED if sorted else DSA_TOPK_POSITION_ORDER, pad_value, _stream())
     return out
 

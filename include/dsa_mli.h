@@ -95,16 +95,21 @@ int dsa_indexer_scan(const void* q_fp8, const float* w, const void* index_k,
  * page_table != NULL: each emitted position g is replaced by its KV slot
  * page_table[b*pt_stride + g/64]*64 + g%64 (position order only).
  *   scores  [B, slab_stride] fp32;  out_idx [B, topk] int32
+ *   scratch dsa_topk_scratch_bytes(B, slab_stride) bytes, zero-filled once
+ *           before the first call; every call leaves it zeroed again, so
+ *           calls chain and graph replays need no memset.  Two calls that
+ *           overlap in time must not share a scratch buffer.
  * Requires topk <= 8192 (<= 4096 with DSA_TOPK_SORTED) and
  * slab_stride <= DSA_TOPK_MAX_CTX.
  * Replaces: reference attention_core.py:66-91 (select_topk), and on the GPU
  * tl_topk (tilelang_dsa/topk_selector.py:355-386) and the in-kernel exact
  * select with hp_page_to_slot (K:1097-1144, K:1248-1310).
  */
+size_t dsa_topk_scratch_bytes(int B, int slab_stride);
 int dsa_topk(const float* scores, const int32_t* seq_lens,
-             const int32_t* page_table, int pt_stride, int32_t* out_idx, int B,
-             int slab_stride, int topk, int flags, int32_t pad_value,
-             void* stream);
+             const int32_t* page_table, int pt_stride, void* scratch,
+             int32_t* out_idx, int B, int slab_stride, int topk, int flags,
+             int32_t pad_value, void* stream);
 
 /*
  * (3) Split-K sparse MLA decode over the fp8 latent pool.
@@ -142,6 +147,7 @@ typedef struct dsa_layer_args {
   const void* index_k;      /* [num_idx_pages, 8448] */
   int64_t num_idx_pages;
   float* scores;            /* [B, slab_stride] scratch */
+  void* topk_scratch;       /* dsa_topk_scratch_bytes(B, slab_stride), zeroed once */
   int32_t* next_idx;        /* [B, topk] out: KV slots, -1 pad */
   /* attention operands */
   const void* q_bf16;       /* [B, H, 576] */

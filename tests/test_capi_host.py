@@ -82,13 +82,18 @@ def test_topk_contract(lib):
     from lagged_indexer_dsa_amd._lib import DSA_ERR_INVALID_ARG, DSA_ERR_UNSUPPORTED
 
     f = lib.dsa_topk
-    assert f(16, 16, None, 0, 16, 1, 1000, 0, 0, -1, None) == DSA_ERR_INVALID_ARG
-    assert f(16, 16, None, 0, 16, 1, 1000, 9000, 0, -1, None) == DSA_ERR_UNSUPPORTED
-    assert f(16, 16, None, 0, 16, 1, 1000, 4097, 1, -1, None) == DSA_ERR_UNSUPPORTED
-    assert f(16, 16, None, 0, 16, 1, 300000, 2048, 0, -1, None) == DSA_ERR_UNSUPPORTED
-    assert f(16, 16, 16, 2, 16, 1, 1000, 2048, 0, -1, None) == DSA_ERR_INVALID_ARG  # pt too short
-    assert f(16, 16, 16, 16, 16, 1, 1000, 2048, 1, -1, None) == DSA_ERR_INVALID_ARG  # slots + sorted
-    assert f(16, 16, None, 0, 16, 1, 1000, 16, 3, -1, None) == DSA_ERR_INVALID_ARG
+    assert f(16, 16, None, 0, 16, 16, 1, 1000, 0, 0, -1, None) == DSA_ERR_INVALID_ARG
+    assert f(16, 16, None, 0, 16, 16, 1, 1000, 9000, 0, -1, None) == DSA_ERR_UNSUPPORTED
+    assert f(16, 16, None, 0, 16, 16, 1, 1000, 4097, 1, -1, None) == DSA_ERR_UNSUPPORTED
+    assert f(16, 16, None, 0, 16, 16, 1, 300000, 2048, 0, -1, None) == DSA_ERR_UNSUPPORTED
+    assert f(16, 16, 16, 2, 16, 16, 1, 1000, 2048, 0, -1, None) == DSA_ERR_INVALID_ARG  # pt too short
+    assert f(16, 16, 16, 16, 16, 16, 1, 1000, 2048, 1, -1, None) == DSA_ERR_INVALID_ARG  # slots + sorted
+    assert f(16, 16, None, 0, 16, 16, 1, 1000, 16, 3, -1, None) == DSA_ERR_INVALID_ARG
+    assert f(16, 16, None, 0, None, 16, 1, 1000, 16, 0, -1, None) == DSA_ERR_INVALID_ARG  # no scratch
+    sb = lib.dsa_topk_scratch_bytes
+    assert sb(1, 131072) >= 4 * (4096 + 131072 // 32 + 2 * 4096)
+    assert sb(2, 1000) == 2 * sb(1, 1000)
+    assert sb(1, 300000) == 0
 
 
 def test_mla_contract_and_workspace(lib):
