@@ -179,6 +179,16 @@ def main() -> int:
     t_idx = time_graph(idx_only.replay, reps, torch)
     t_full = time_graph(full.replay, reps, torch)
     hidden = 1.0 - (t_full - t_attn) / t_idx if t_idx > 0 else None
+    # the same schedule without a graph: two streams, and one stream
+    t_eager = time_graph(full.run_eager, reps, torch)
+
+    def serial():
+        att = first
+        for L in layers:
+            L.run(attend_idx=att)
+            if L.has_indexer:
+                att = L.next_idx
+    t_serial = time_graph(serial, reps, torch)
 
     # ---- dominant kernel: indexer scan, per-launch HIP events ----
     L0 = layers[0]
@@ -223,7 +233,8 @@ def main() -> int:
                       "sparse_mla+combine": round(attn_ms * 1e3, 3),
                       "indexer_scan_event_pairs": round(scan_ms_pairs * 1e3, 3)},
         "attention_gather_GBps": round(ab / (attn_ms * 1e-3) / 1e9, 1),
-        "mli": {"graph_ms": round(t_full, 5), "attn_only_ms": round(t_attn, 5),
+        "mli": {"graph_ms": round(t_full, 5), "eager_2stream_ms": round(t_eager, 5),
+                "serial_1stream_ms": round(t_serial, 5), "attn_only_ms": round(t_attn, 5),
                 "indexer_only_ms": round(t_idx, 5),
                 "hidden_fraction": None if hidden is None else round(hidden, 4)},
         "roofline": {"bound": "hbm", "achieved": round(scan_gbs, 1), "peak": HBM_PEAK_GBS,

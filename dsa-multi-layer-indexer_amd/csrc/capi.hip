@@ -1,5 +1,5 @@
 // C ABI of libdsa_mli.so: argument contracts, the decode-layer composite and
-// the MLI two-stream schedule (eager and captured as one hipGraph).
+// the MLI schedule (eager and captured as one hipGraph).
 //
 // Contract checks mirror the reference launcher's TORCH_CHECKs
 // (kernels/cuda_fused_sparse_splitk.py K:2399-2611) as negative return codes;
@@ -11,22 +11,7 @@
 #include <vector>
 
 #include "dsa_common.h"
-
-namespace dsa {
-hipError_t launch_indexer_scan(const uint8_t* q8, const float* w, const uint8_t* pages,
-                               long num_pages, const int* pt, const int* seq_lens, float* scores,
-                               int B, int Hidx, int pt_stride, int slab_stride, hipStream_t s);
-void set_scan_variant(int v);
-hipError_t launch_topk(const float* scores, const int* seq_lens, const int* page_table,
-                       int pt_stride, void* scratch, int* out, int B, int slab, int K, int sorted,
-                       int pad, hipStream_t s);
-size_t topk_scratch_bytes(int B, int slab);
-hipError_t launch_sparse_mla(const uint16_t* q, const uint8_t* pool, long kv_rows,
-                             const int* idx, void* workspace, uint16_t* out, int B, int H,
-                             int topk, int nsplit, float sm_scale, hipStream_t s);
-int sparse_mla_auto_nsplit(int topk);
-size_t sparse_mla_workspace_bytes(int B, int H, int nsplit);
-}  // namespace dsa
+#include "dsa_kernels.h"
 
 namespace {
 
@@ -50,6 +35,8 @@ int hip_status(hipError_t e, const char* what) {
     if (!(cond)) return fail(code, __VA_ARGS__); \
   } while (0)
 
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
 int check_scan(const void* q_fp8, const float* w, const void* index_k, int64_t num_pages,
                const int32_t* page_table, const int32_t* seq_lens, const float* scores, int B,
                int Hidx, int pt_stride, int slab_stride) {
@@ -62,8 +49,8 @@ int check_scan(const void* q_fp8, const float* w, const void* index_k, int64_t n
   DSA_REQUIRE(num_pages >= 1, DSA_ERR_INVALID_ARG, "dsa_indexer_scan: num_pages must be >= 1");
   DSA_REQUIRE(pt_stride >= 1, DSA_ERR_INVALID_ARG, "dsa_indexer_scan: pt_stride must be >= 1");
   DSA_REQUIRE(slab_stride >= 1, DSA_ERR_INVALID_ARG, "dsa_indexer_scan: slab_stride must be >= 1");
-  DSA_REQUIRE(((uintptr_t)q_fp8 & 15) == 0 && ((uintptr_t)index_k & 15) == 0,
-              DSA_ERR_INVALID_ARG, "dsa_indexer_scan: q_fp8 and index_k must be 16-byte aligned");
+  DSA_REQUIRE(aligned16(q_fp8) && aligned16(index_k), DSA_ERR_INVALID_ARG,
+              "dsa_indexer_scan: q_fp8 and index_k must be 16-byte aligned");
   return DSA_OK;
 }
 
@@ -72,9 +59,8 @@ int check_topk(const float* scores, const int32_t* seq_lens, const int32_t* page
                int slab_stride, int topk, int flags) {
   DSA_REQUIRE(scores && seq_lens && out_idx && scratch, DSA_ERR_INVALID_ARG,
               "dsa_topk: null pointer argument");
-  DSA_REQUIRE(((uintptr_t)scratch & 15) == 0, DSA_ERR_INVALID_ARG,
-              "dsa_topk: scratch must be 16-byte aligned");
-  DSA_REQUIRE(B >= 1, DSA_ERR_INVALID_ARG, "dsa_topk: B must be >= 1 (got %d)", B);
+  DSA_REQUIRE(aligned16(scratch), DSA_ERR_INVALID_ARG, "dsa_topk: scratch must be 16-byte aligned");
+  DSA_REQUIRE(B >= 1 && B <= 65535, DSA_ERR_INVALID_ARG, "dsa_topk: B must be in [1, 65535] (got %d)", B);
   DSA_REQUIRE(topk >= 1, DSA_ERR_INVALID_ARG, "dsa_topk: topk must be >= 1 (got %d)", topk);
   DSA_REQUIRE(flags == DSA_TOPK_POSITION_ORDER || flags == DSA_TOPK_SORTED, DSA_ERR_INVALID_ARG,
               "dsa_topk: unknown flags %d", flags);
@@ -92,8 +78,8 @@ int check_topk(const float* scores, const int32_t* seq_lens, const int32_t* page
 int check_mla(const void* q_bf16, const void* kv_pool, int64_t kv_rows, const int32_t* idx,
               const void* workspace, const void* out_bf16, int B, int H, int topk, int nsplit,
               bool idx_required = true) {
-  DSA_REQUIRE(q_bf16 && kv_pool && (idx || !idx_required) && workspace && out_bf16, DSA_ERR_INVALID_ARG,
-              "dsa_sparse_mla_decode: null pointer argument");
+  DSA_REQUIRE(q_bf16 && kv_pool && (idx || !idx_required) && workspace && out_bf16,
+              DSA_ERR_INVALID_ARG, "dsa_sparse_mla_decode: null pointer argument");
   DSA_REQUIRE(B >= 1 && B <= 65535, DSA_ERR_INVALID_ARG, "dsa_sparse_mla_decode: bad B %d", B);
   DSA_REQUIRE(H >= 16 && H % 16 == 0 && H <= 16 * 64, DSA_ERR_UNSUPPORTED,
               "dsa_sparse_mla_decode: H must be a positive multiple of 16 (got %d)", H);
@@ -101,14 +87,14 @@ int check_mla(const void* q_bf16, const void* kv_pool, int64_t kv_rows, const in
   DSA_REQUIRE(nsplit >= 0 && nsplit <= 128, DSA_ERR_UNSUPPORTED,
               "dsa_sparse_mla_decode: nsplit must be in [0, 128] (got %d)", nsplit);
   DSA_REQUIRE(kv_rows >= 1, DSA_ERR_INVALID_ARG, "dsa_sparse_mla_decode: kv_rows must be >= 1");
-  DSA_REQUIRE(((uintptr_t)q_bf16 & 15) == 0 && ((uintptr_t)kv_pool & 15) == 0 &&
-                  ((uintptr_t)workspace & 15) == 0 && ((uintptr_t)out_bf16 & 7) == 0,
+  DSA_REQUIRE(aligned16(q_bf16) && aligned16(kv_pool) && aligned16(workspace) &&
+                  ((uintptr_t)out_bf16 & 7) == 0,
               DSA_ERR_INVALID_ARG, "dsa_sparse_mla_decode: q/kv_pool/workspace must be 16-byte aligned");
   return DSA_OK;
 }
 
 int resolve_nsplit(int nsplit, int topk) {
-  return nsplit > 0 ? nsplit : dsa::sparse_mla_auto_nsplit(topk);
+  return nsplit > 0 ? nsplit : dsa::attn_auto_nsplit(topk);
 }
 
 // in_schedule: attend_idx == NULL is resolved by the MLI schedule (the most
@@ -135,69 +121,96 @@ int check_layer(const dsa_layer_args* a, bool in_schedule = false) {
   return DSA_OK;
 }
 
-int enqueue_indexer(const dsa_layer_args* a, hipStream_t s) {
-  int rc = hip_status(
-      dsa::launch_indexer_scan((const uint8_t*)a->q_fp8, a->w, (const uint8_t*)a->index_k,
-                               (long)a->num_idx_pages, a->page_table, a->seq_lens, a->scores, a->B,
-                               a->Hidx, a->pt_stride, a->slab_stride, s),
-      "indexer scan launch");
+dsa::AttnArgs attn_args(const void* q_bf16, const void* kv_pool, int64_t kv_rows,
+                        const int32_t* idx, void* workspace, void* out_bf16, int B, int H,
+                        int topk, int nsplit, float sm_scale) {
+  dsa::AttnArgs A{};
+  A.q = (const uint16_t*)q_bf16;
+  A.pool = (const uint8_t*)kv_pool;
+  A.kv_rows = (long)kv_rows;
+  A.idx = idx;
+  A.out = (uint16_t*)out_bf16;
+  A.H = H;
+  A.topk = topk;
+  A.nsplit = resolve_nsplit(nsplit, topk);
+  A.sm_log2 = sm_scale * 1.4426950408889634f;
+  dsa::attn_bind_workspace(A, workspace, B);
+  return A;
+}
+
+dsa::ScanArgs scan_args(const void* q_fp8, const float* w, const void* index_k, int64_t num_pages,
+                        const int32_t* page_table, const int32_t* seq_lens, float* scores,
+                        int Hidx, int pt_stride, int slab_stride, void* topk_scratch,
+                        int32_t* next_idx = nullptr, int topk = 0) {
+  dsa::ScanArgs S{};
+  S.q8 = (const uint8_t*)q_fp8;
+  S.w = w;
+  S.pages = (const uint8_t*)index_k;
+  S.num_pages = (long)num_pages;
+  S.page_table = page_table;
+  S.seq_lens = seq_lens;
+  S.scores = scores;
+  S.hist = (uint32_t*)topk_scratch;
+  S.hist_row_words = dsa::topk_row_words(slab_stride);
+  S.next_idx = next_idx;
+  S.topk = topk;
+  S.pt_stride = pt_stride;
+  S.slab_stride = slab_stride;
+  S.Hidx = Hidx;
+  return S;
+}
+
+// One layer on one stream.  attend: the selection its attention reads
+// (nullptr: no attention); with_indexer: scan + select into next_idx, both
+// in the decode launch (the row's last scan workgroup selects).  When the
+// attention reads this layer's own fresh selection, it is a second launch.
+int enqueue_layer(const dsa_layer_args* a, const int32_t* attend, bool with_indexer,
+                  hipStream_t s) {
+  dsa::AttnArgs A{};
+  dsa::ScanArgs S{};
+  const bool attention = a->q_bf16 != nullptr && attend != nullptr;
+  if (attention)
+    A = attn_args(a->q_bf16, a->kv_pool, a->kv_rows, attend, a->workspace, a->out_bf16, a->B,
+                  a->H, a->topk, a->nsplit, a->sm_scale);
+  if (with_indexer)
+    S = scan_args(a->q_fp8, a->w, a->index_k, a->num_idx_pages, a->page_table, a->seq_lens,
+                  a->scores, a->Hidx, a->pt_stride, a->slab_stride, a->topk_scratch, a->next_idx,
+                  a->topk);
+  const bool own = attention && with_indexer && attend == a->next_idx;
+  int rc = hip_status(dsa::launch_decode_main(attention && !own ? &A : nullptr, a->B,
+                                              with_indexer ? &S : nullptr, a->B, s),
+                      "decode main launch");
   if (rc) return rc;
-  return hip_status(dsa::launch_topk(a->scores, a->seq_lens, a->page_table, a->pt_stride,
-                                     a->topk_scratch, a->next_idx, a->B, a->slab_stride, a->topk,
-                                     0, -1, s),
-                    "top-k launch");
+  if (own) rc = hip_status(dsa::launch_decode_main(&A, a->B, nullptr, 0, s), "attention launch");
+  return rc;
 }
 
-int enqueue_attention(const dsa_layer_args* a, const int32_t* att, hipStream_t s) {
-  return hip_status(
-      dsa::launch_sparse_mla((const uint16_t*)a->q_bf16, (const uint8_t*)a->kv_pool,
-                             (long)a->kv_rows, att, a->workspace, (uint16_t*)a->out_bf16, a->B,
-                             a->H, a->topk, resolve_nsplit(a->nsplit, a->topk), a->sm_scale, s),
-      "sparse MLA launch");
-}
-
-// Enqueue the MLI schedule: attention on `main`, indexers on `side`.
-//   indexer(i) waits for attention(i-1) (its query comes from layer i's input);
-//   attention(i) waits for the indexer whose selection it consumes.
-int enqueue_mli(const dsa_layer_args* layers, int n, hipStream_t main, hipStream_t side,
-                std::vector<hipEvent_t>& events) {
-  auto new_event = [&](hipEvent_t* e) -> int {
-    hipError_t err = hipEventCreateWithFlags(e, hipEventDisableTiming);
-    if (err != hipSuccess) return hip_status(err, "hipEventCreate");
-    events.push_back(*e);
-    return DSA_OK;
-  };
-  int rc;
-  const int32_t* carried = nullptr;   // selection available to the next layer
-  hipEvent_t carried_ev = nullptr;     // side-stream event that produced it
-  hipEvent_t side_tail = nullptr;      // last event recorded on side
+// The MLI schedule on one stream: layer i = ONE launch running attention(i)
+// over the carried selection side by side with indexer-scan(i) + top-k(i),
+// whose selection layer i+1's attention consumes.
+int enqueue_mli(const dsa_layer_args* layers, int n, hipStream_t s) {
+  const int32_t* carried = nullptr;
   for (int i = 0; i < n; ++i) {
     const dsa_layer_args* a = &layers[i];
     const int32_t* att = a->attend_idx ? a->attend_idx : carried;
-    hipEvent_t att_ev = a->attend_idx ? nullptr : carried_ev;
-    if (a->q_fp8) {
-      hipEvent_t fork;
-      if ((rc = new_event(&fork))) return rc;
-      if ((rc = hip_status(hipEventRecord(fork, main), "hipEventRecord"))) return rc;
-      if ((rc = hip_status(hipStreamWaitEvent(side, fork, 0), "hipStreamWaitEvent"))) return rc;
-      if ((rc = enqueue_indexer(a, side))) return rc;
-      hipEvent_t done;
-      if ((rc = new_event(&done))) return rc;
-      if ((rc = hip_status(hipEventRecord(done, side), "hipEventRecord"))) return rc;
-      carried = a->next_idx;
-      carried_ev = done;
-      side_tail = done;
-    }
-    if (a->q_bf16) {
-      if (!att) return fail(DSA_ERR_INVALID_ARG, "mli layer %d: no selection to attend", i);
-      if (att_ev && (rc = hip_status(hipStreamWaitEvent(main, att_ev, 0), "hipStreamWaitEvent")))
-        return rc;
-      if ((rc = enqueue_attention(a, att, main))) return rc;
-    }
+    if (a->q_bf16 && !att) return fail(DSA_ERR_INVALID_ARG, "mli layer %d: no selection to attend", i);
+    const int rc = enqueue_layer(a, a->q_bf16 ? att : nullptr, a->q_fp8 != nullptr, s);
+    if (rc) return rc;
+    if (a->q_fp8) carried = a->next_idx;
   }
-  // join the side stream back so the schedule ends on `main`
-  if (side_tail && (rc = hip_status(hipStreamWaitEvent(main, side_tail, 0), "hipStreamWaitEvent")))
-    return rc;
+  return DSA_OK;
+}
+
+int check_mli(const dsa_layer_args* layers, int n) {
+  DSA_REQUIRE(layers && n >= 1, DSA_ERR_INVALID_ARG, "mli: need at least one layer");
+  const int32_t* carried = nullptr;
+  for (int i = 0; i < n; ++i) {
+    const int rc = check_layer(&layers[i], true);
+    if (rc) return rc;
+    if (layers[i].q_bf16 && !layers[i].attend_idx && !carried)
+      return fail(DSA_ERR_INVALID_ARG, "mli layer %d: attend_idx is NULL and no earlier layer indexes", i);
+    if (layers[i].q_fp8) carried = layers[i].next_idx;
+  }
   return DSA_OK;
 }
 
@@ -206,15 +219,13 @@ int enqueue_mli(const dsa_layer_args* layers, int n, hipStream_t main, hipStream
 struct dsa_mli_graph {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
-  hipStream_t side = nullptr;
-  std::vector<hipEvent_t> events;
 };
 
 extern "C" {
 
 const char* dsa_last_error(void) { return g_err; }
 
-const char* dsa_version(void) { return "dsa_mli 0.1.0 gfx950"; }
+const char* dsa_version(void) { return "dsa_mli 0.2.0 gfx950"; }
 
 int dsa_indexer_scan(const void* q_fp8, const float* w, const void* index_k, int64_t num_pages,
                      const int32_t* page_table, const int32_t* seq_lens, float* scores, int B,
@@ -222,9 +233,9 @@ int dsa_indexer_scan(const void* q_fp8, const float* w, const void* index_k, int
   int rc = check_scan(q_fp8, w, index_k, num_pages, page_table, seq_lens, scores, B, Hidx,
                       pt_stride, slab_stride);
   if (rc) return rc;
-  return hip_status(dsa::launch_indexer_scan((const uint8_t*)q_fp8, w, (const uint8_t*)index_k,
-                                             (long)num_pages, page_table, seq_lens, scores, B,
-                                             Hidx, pt_stride, slab_stride, (hipStream_t)stream),
+  dsa::ScanArgs S = scan_args(q_fp8, w, index_k, num_pages, page_table, seq_lens, scores, Hidx,
+                              pt_stride, slab_stride, nullptr);
+  return hip_status(dsa::launch_decode_main(nullptr, 0, &S, B, (hipStream_t)stream),
                     "indexer scan launch");
 }
 
@@ -239,15 +250,19 @@ int dsa_topk(const float* scores, const int32_t* seq_lens, const int32_t* page_t
   int rc = check_topk(scores, seq_lens, page_table, pt_stride, scratch, out_idx, B, slab_stride,
                       topk, flags);
   if (rc) return rc;
-  return hip_status(dsa::launch_topk(scores, seq_lens, page_table, pt_stride, scratch, out_idx, B,
-                                     slab_stride, topk, flags == DSA_TOPK_SORTED, pad_value,
-                                     (hipStream_t)stream),
-                    "top-k launch");
+  hipStream_t s = (hipStream_t)stream;
+  rc = hip_status(dsa::launch_topk_hist(scores, seq_lens, scratch, B, slab_stride, topk, s),
+                  "top-k histogram launch");
+  if (rc) return rc;
+  return hip_status(dsa::launch_topk_select(scores, seq_lens, page_table, pt_stride, scratch,
+                                            out_idx, B, slab_stride, topk,
+                                            flags == DSA_TOPK_SORTED, pad_value, s),
+                    "top-k select launch");
 }
 
 size_t dsa_sparse_mla_workspace_bytes(int B, int H, int nsplit) {
-  if (B < 1 || H < 16 || H % 16 || nsplit < 0 || nsplit > 128) return 0;
-  return dsa::sparse_mla_workspace_bytes(B, H, nsplit > 0 ? nsplit : 128);
+  if (B < 1 || B > 65535 || H < 16 || H % 16 || H > 16 * 64 || nsplit < 0 || nsplit > 128) return 0;
+  return dsa::attn_workspace_bytes(B, H, nsplit > 0 ? nsplit : 128);
 }
 
 int dsa_sparse_mla_decode(const void* q_bf16, const void* kv_pool, int64_t kv_rows,
@@ -255,46 +270,24 @@ int dsa_sparse_mla_decode(const void* q_bf16, const void* kv_pool, int64_t kv_ro
                           int topk, int nsplit, float sm_scale, void* stream) {
   int rc = check_mla(q_bf16, kv_pool, kv_rows, idx, workspace, out_bf16, B, H, topk, nsplit);
   if (rc) return rc;
-  return hip_status(dsa::launch_sparse_mla((const uint16_t*)q_bf16, (const uint8_t*)kv_pool,
-                                           (long)kv_rows, idx, workspace, (uint16_t*)out_bf16, B,
-                                           H, topk, resolve_nsplit(nsplit, topk), sm_scale,
-                                           (hipStream_t)stream),
+  dsa::AttnArgs A = attn_args(q_bf16, kv_pool, kv_rows, idx, workspace, out_bf16, B, H, topk,
+                              nsplit, sm_scale);
+  return hip_status(dsa::launch_decode_main(&A, B, nullptr, 0, (hipStream_t)stream),
                     "sparse MLA launch");
 }
 
 int dsa_decode_layer(const dsa_layer_args* args, void* stream) {
   int rc = check_layer(args);
   if (rc) return rc;
-  hipStream_t s = (hipStream_t)stream;
-  if (args->q_fp8 && (rc = enqueue_indexer(args, s))) return rc;
-  if (args->q_bf16)
-    return enqueue_attention(args, args->attend_idx ? args->attend_idx : args->next_idx, s);
-  return DSA_OK;
+  const int32_t* att = args->attend_idx ? args->attend_idx : args->next_idx;
+  return enqueue_layer(args, args->q_bf16 ? att : nullptr, args->q_fp8 != nullptr,
+                       (hipStream_t)stream);
 }
 
-static int check_mli(const dsa_layer_args* layers, int n) {
-  DSA_REQUIRE(layers && n >= 1, DSA_ERR_INVALID_ARG, "mli: need at least one layer");
-  const int32_t* carried = nullptr;
-  for (int i = 0; i < n; ++i) {
-    int rc = check_layer(&layers[i], true);
-    if (rc) return rc;
-    if (layers[i].q_bf16 && !layers[i].attend_idx && !carried)
-      return fail(DSA_ERR_INVALID_ARG, "mli layer %d: attend_idx is NULL and no earlier layer indexes", i);
-    if (layers[i].q_fp8) carried = layers[i].next_idx;
-  }
-  return DSA_OK;
-}
-
-int dsa_mli_run_eager(const dsa_layer_args* layers, int num_layers, void* stream,
-                      void* side_stream) {
+int dsa_mli_run_eager(const dsa_layer_args* layers, int num_layers, void* stream) {
   int rc = check_mli(layers, num_layers);
   if (rc) return rc;
-  DSA_REQUIRE(side_stream && side_stream != stream, DSA_ERR_INVALID_ARG,
-              "dsa_mli_run_eager: side_stream must be a distinct non-null stream");
-  std::vector<hipEvent_t> events;
-  rc = enqueue_mli(layers, num_layers, (hipStream_t)stream, (hipStream_t)side_stream, events);
-  for (hipEvent_t e : events) (void)hipEventDestroy(e);
-  return rc;
+  return enqueue_mli(layers, num_layers, (hipStream_t)stream);
 }
 
 int dsa_mli_graph_create(const dsa_layer_args* layers, int num_layers, void* capture_stream,
@@ -303,27 +296,18 @@ int dsa_mli_graph_create(const dsa_layer_args* layers, int num_layers, void* cap
   *out_graph = nullptr;
   int rc = check_mli(layers, num_layers);
   if (rc) return rc;
-  hipStream_t main = (hipStream_t)capture_stream;
-  bool own_main = false;
-  if (main == nullptr) {
-    if ((rc = hip_status(hipStreamCreateWithFlags(&main, hipStreamNonBlocking), "hipStreamCreate")))
-      return rc;
-    own_main = true;
-  }
+  DSA_REQUIRE(capture_stream, DSA_ERR_INVALID_ARG,
+              "dsa_mli_graph_create: capture_stream must be a non-null stream");
+  hipStream_t s = (hipStream_t)capture_stream;
   dsa_mli_graph* g = new dsa_mli_graph();
-  rc = hip_status(hipStreamCreateWithFlags(&g->side, hipStreamNonBlocking), "hipStreamCreate");
-  if (!rc) rc = hip_status(hipStreamBeginCapture(main, hipStreamCaptureModeThreadLocal),
-                           "hipStreamBeginCapture");
+  rc = hip_status(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
   if (!rc) {
-    int erc = enqueue_mli(layers, num_layers, main, g->side, g->events);
-    hipGraph_t graph = nullptr;
-    int crc = hip_status(hipStreamEndCapture(main, &graph), "hipStreamEndCapture");
+    const int erc = enqueue_mli(layers, num_layers, s);
+    const int crc = hip_status(hipStreamEndCapture(s, &g->graph), "hipStreamEndCapture");
     rc = erc ? erc : crc;
-    g->graph = graph;
     if (!rc) rc = hip_status(hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0),
                              "hipGraphInstantiate");
   }
-  if (own_main) (void)hipStreamDestroy(main);
   if (rc) {
     dsa_mli_graph_destroy(g);
     return rc;
@@ -341,10 +325,27 @@ int dsa_mli_graph_destroy(dsa_mli_graph* graph) {
   if (!graph) return DSA_OK;
   if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
   if (graph->graph) (void)hipGraphDestroy(graph->graph);
-  for (hipEvent_t e : graph->events) (void)hipEventDestroy(e);
-  if (graph->side) (void)hipStreamDestroy(graph->side);
   delete graph;
   return DSA_OK;
+}
+
+// Internal (not in the public header): phase timestamps.  on=1 clears and
+// enables, on=0 disables; read copies n words (n <= 512*16) of the table.
+int dsa_internal_debug(int on) {
+  const int v = on ? 1 : 0;
+  hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(dsa::g_dbg_on), &v, sizeof(v));
+  if (e == hipSuccess && on) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(dsa::g_dbg));
+    if (e == hipSuccess) e = hipMemset(p, 0, sizeof(unsigned long long) * dsa::kDbgBlocks * dsa::kDbgPhases);
+  }
+  return hip_status(e, "debug enable");
+}
+
+int dsa_internal_debug_read(unsigned long long* host, int n) {
+  n = std::max(0, std::min(n, dsa::kDbgBlocks * dsa::kDbgPhases));
+  return hip_status(hipMemcpyFromSymbol(host, HIP_SYMBOL(dsa::g_dbg), n * sizeof(unsigned long long)),
+                    "debug read");
 }
 
 // Internal (not in the public header): selects the fp8 MFMA form of the scan.

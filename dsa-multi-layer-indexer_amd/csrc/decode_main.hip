@@ -1,0 +1,649 @@
+// The decode layer's main launch (gfx950): sparse-MLA attention workgroups
+// and lightning-indexer scan workgroups in ONE grid.
+//
+// Roles by blockIdx.x (role-decoupled workgroups, as the reference's HIDE
+// kernel does, K:1047-1070):
+//   [0, n_att)         attention: (row, head group, split) of split-K sparse
+//                      MLA; the last workgroup of a (row, head group) to
+//                      finish merges the splits (log-sum-exp) into the
+//                      output -- an arrival counter, no waiting;
+//   [n_att, +n_scan)   indexer scan: (row, slice) of the row's 16-key
+//                      chunks; adds its scores' 12-bit key histogram to the
+//                      row's top-k histogram, and the row's last scan
+//                      workgroup to finish (arrival counter) runs the
+//                      row's whole top-k select (topk.hip finalize_row,
+//                      one pass over the scores) while attention blocks
+//                      are still gathering.
+// Under the MLI lag, layer L's attention (over layer L-1's selection) and
+// layer L's indexer scan are independent, so one grid runs both and the
+// scan's HBM stream hides under the attention's gather latency.  Measured on
+// MI355X: two HIP streams, or one hipGraph with two branches, did not run
+// these concurrently (the host dispatches one node at a time), while one
+// grid does by construction.
+//
+// Attention (reference hp_attention_block K:1312-1598, combine K:996-1045,
+// CPU semantics attention_core.py:94-146):
+//   out[b,h,:] = sum_j softmax_j(sm * q[b,h,:] . kv_j) * kv_j[:512],
+//   kv_j = bf16_rn(f32(e4m3) * scale[d/128]) | bf16 rope (K:1181-1197).
+// A workgroup (8 waves) takes 128-key tiles of its split.  Lane (kr, kc) of
+// wave w gathers key 16w+kr's bytes [128kc, +128) + scale kc + rope
+// [16kc, +16) straight into registers (4 lanes per 656-byte row, each a
+// contiguous run), dequantises them and feeds them as the B operand of
+// v_mfma_f32_16x16x32_bf16 with the 16 heads as A; Q and K use the same
+// lane->k assignment, so the 576-dim contraction needs no LDS staging.
+// The value tile is written to LDS transposed ([dim][key]) for the PV MFMA;
+// softmax runs in the exp2 domain.
+//
+// Scan (reference hp_indexer_block K:1677-2157, fp8 semantics K:2990-2992):
+//   score[b,g] = kscale[g] * sum_h w[b,h] * ReLU(q[b,h,:] . k[g,:]).
+// A wave owns 16-key chunks (2 KB contiguous in an 8448-byte page); one
+// v_mfma_f32_16x16x128_f8f6f4 per 16 heads contracts the whole 128-d dot
+// product (A = query heads, B = key chunk, loaded straight from HBM into
+// registers with the same lane->k assignment as A).  Each lane ends with one
+// key x 4 heads: ReLU*w summed in-lane, then across lane groups with two xor
+// shuffles.  Up to kScanBatch chunks per wave have loads in flight.
+#include <algorithm>
+
+#include "dsa_common.h"
+#include "dsa_kernels.h"
+
+namespace dsa {
+
+constexpr int kMainThreads = 512;
+constexpr int kMainWaves = kMainThreads / kWave;  // 8
+
+// ======================================================================
+// attention role
+// ======================================================================
+constexpr int kTile = 16 * kMainWaves;  // 128 keys per tile
+constexpr int kVLd = DSA_LATENT_DIM + 16;  // value tile row stride (bf16): 264 dwords, 8 mod 64 banks
+constexpr int kPLd = kTile + 8;         // probability row stride (bf16)
+constexpr int kHG = 16;                 // heads per group
+constexpr int kMaxSplit = 128;
+
+struct AttnShared {
+  uint16_t vt[kTile * kVLd];             // value tile [key][dim], row-major
+  float s[kHG * kTile];                  // scores, log2 domain
+  uint16_t p[kHG * kPLd];                // probabilities, bf16
+  float m[kHG], l[kHG], alpha[kHG];
+  uint32_t last;
+};
+static_assert(kMaxSplit * 3 * kHG * sizeof(float) <= sizeof(AttnShared::vt), "merge scratch");
+
+__device__ __forceinline__ v4f mfma_bf16(const uint4& a, const uint4& b, v4f c) {
+  v8bf av, bv;
+  __builtin_memcpy(&av, &a, 16);
+  __builtin_memcpy(&bv, &b, 16);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, c, 0, 0, 0);
+}
+
+// 16 e4m3 (one uint4) * scale -> 16 bf16 (two uint4: elements 0-7, 8-15),
+// bf16_rn(f32(e4m3) * scale) exactly.
+__device__ __forceinline__ void dequant16(const uint4& v, float sc, uint4& lo, uint4& hi) {
+  float f[16];
+  e4m3x4_to_f32(v.x, f + 0);
+  e4m3x4_to_f32(v.y, f + 4);
+  e4m3x4_to_f32(v.z, f + 8);
+  e4m3x4_to_f32(v.w, f + 12);
+  lo.x = pack_bf16x2(f[0] * sc, f[1] * sc);
+  lo.y = pack_bf16x2(f[2] * sc, f[3] * sc);
+  lo.z = pack_bf16x2(f[4] * sc, f[5] * sc);
+  lo.w = pack_bf16x2(f[6] * sc, f[7] * sc);
+  hi.x = pack_bf16x2(f[8] * sc, f[9] * sc);
+  hi.y = pack_bf16x2(f[10] * sc, f[11] * sc);
+  hi.z = pack_bf16x2(f[12] * sc, f[13] * sc);
+  hi.w = pack_bf16x2(f[14] * sc, f[15] * sc);
+}
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+
+// B operand of the PV MFMA (k = 32 keys, n = 16 dims) from the row-major
+// value tile with two ds_read_b64_tr_b16.  Within each 16-lane group that
+// instruction hands lane i element (i & 3) of the 8-byte word addressed by
+// lane 4j + (i >> 2), as element j.  So lane (a, g) of k-group g addresses
+// key 8g + (a >> 2) (+4 for the second read), dims col0 + 4(a & 3): lane n
+// then holds V[8g + 0..7][col0 + n], k-slots 8g..8g+7 -- the same k-slot ->
+// key map the probabilities' A operand uses (P[h][32ks + 8g + e]).
+__device__ __forceinline__ uint4 load_v_operand(const uint16_t* vt, int key0, int col0, int lane) {
+  const int a = lane & 15, g = lane >> 4;
+  const uint16_t* p = vt + (key0 + 8 * g + (a >> 2)) * kVLd + col0 + 4 * (a & 3);
+  typedef v4s __attribute__((address_space(3)))* lds_v4s;
+  const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(p));
+  const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(p + 4 * kVLd));
+  uint4 r;
+  __builtin_memcpy(&r.x, &lo, 8);
+  __builtin_memcpy(&r.z, &hi, 8);
+  return r;
+}
+
+__device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg, int sp, unsigned char* smem) {
+  AttnShared& sh = *reinterpret_cast<AttnShared*>(smem);
+  const int nhg = A.H / kHG, nsplit = A.nsplit;
+  const int dbk = blockIdx.x;
+  dbg_stamp(dbk, 0);
+  const int t = threadIdx.x;
+  const int lane = t & (kWave - 1);
+  const int wv = wave_id();
+  const int kr = lane & 15, kc = lane >> 4;
+  const int kps = (A.topk + nsplit - 1) / nsplit;
+  const int k0 = min(A.topk, sp * kps), k1 = min(A.topk, k0 + kps);
+  const int* idx_row = A.idx + (long)b * A.topk;
+
+  // first tile's slot before the query (the gather depends on it)
+  int slot_next = (k0 + 16 * wv + kr < k1) ? idx_row[k0 + 16 * wv + kr] : -1;
+
+  // Q (A operand): step s<16 -> dims 128kc + 8s; s = 16, 17 -> 512 + 16kc + 8(s-16)
+  uint4 qa[18];
+  {
+    const uint16_t* qrow = A.q + ((long)b * A.H + hg * kHG + kr) * DSA_QK_DIM;
+#pragma unroll
+    for (int s = 0; s < 16; ++s) qa[s] = *reinterpret_cast<const uint4*>(qrow + 128 * kc + 8 * s);
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+      qa[16 + s] = *reinterpret_cast<const uint4*>(qrow + DSA_LATENT_DIM + 16 * kc + 8 * s);
+  }
+  if (t < kHG) { sh.m[t] = -INFINITY; sh.l[t] = 0.f; }
+
+  v4f o[4];  // wave owns output dims [64 wv, 64 wv + 64): 4 n-tiles
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) o[nt] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  for (int tile0 = k0; tile0 < k1; tile0 += kTile) {
+    const int slot = slot_next;
+    const bool valid = slot >= 0 && (long)slot < A.kv_rows;
+    const uint8_t* rowp = A.pool + (valid ? (long)slot : 0L) * DSA_LATENT_ROW_BYTES;
+    uint4 nope[8], rope[2];
+    float sc = 0.f;
+    if (valid) {
+      const uint4* np = reinterpret_cast<const uint4*>(rowp + 128 * kc);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) nope[i] = np[i];
+      sc = reinterpret_cast<const float*>(rowp + DSA_LATENT_DIM)[kc];
+      const uint4* rp = reinterpret_cast<const uint4*>(rowp + DSA_LATENT_DIM + 16 + 32 * kc);
+      rope[0] = rp[0];
+      rope[1] = rp[1];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) nope[i] = make_uint4(0, 0, 0, 0);
+      rope[0] = rope[1] = make_uint4(0, 0, 0, 0);
+    }
+    {
+      const int jn = tile0 + kTile + 16 * wv + kr;  // next tile's slot, early
+      slot_next = (jn < k1) ? idx_row[jn] : -1;
+    }
+
+    // dequantise -> QK MFMA + row-major value tile (16-byte stores)
+    const int kl = 16 * wv + kr;
+    uint4* vrow = reinterpret_cast<uint4*>(sh.vt + kl * kVLd + 128 * kc);
+    v4f sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      uint4 lo, hi;
+      dequant16(nope[i], sc, lo, hi);
+      sacc = mfma_bf16(qa[2 * i], lo, sacc);
+      sacc = mfma_bf16(qa[2 * i + 1], hi, sacc);
+      vrow[2 * i] = lo;
+      vrow[2 * i + 1] = hi;
+    }
+    sacc = mfma_bf16(qa[16], rope[0], sacc);
+    sacc = mfma_bf16(qa[17], rope[1], sacc);
+    dbg_stamp(dbk, 1);
+    // lane holds key kl (column), heads 4kc + r (rows)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      sh.s[(4 * kc + r) * kTile + kl] = valid ? sacc[r] * A.sm_log2 : -INFINITY;
+    __syncthreads();
+
+    // online softmax: thread t -> head t/32, keys 4*(t%32) .. +4
+    {
+      const int h = t >> 5, q4 = (t & 31) * 4;
+      float sv[4];
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) { sv[i] = sh.s[h * kTile + q4 + i]; tmax = fmaxf(tmax, sv[i]); }
+#pragma unroll
+      for (int off = 1; off < 32; off <<= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, off));
+      const float m_old = sh.m[h];
+      const float m_new = fmaxf(m_old, tmax);
+      const float alpha = (m_new == -INFINITY) ? 1.f : exp2f(m_old - m_new);
+      float psum = 0.f;
+      uint32_t pw[2];
+#pragma unroll
+      for (int i = 0; i < 4; i += 2) {
+        const float p0 = (sv[i] == -INFINITY) ? 0.f : exp2f(sv[i] - m_new);
+        const float p1 = (sv[i + 1] == -INFINITY) ? 0.f : exp2f(sv[i + 1] - m_new);
+        psum += p0 + p1;
+        pw[i >> 1] = pack_bf16x2(p0, p1);
+      }
+#pragma unroll
+      for (int off = 1; off < 32; off <<= 1) psum += __shfl_xor(psum, off);
+      uint32_t* prow = reinterpret_cast<uint32_t*>(sh.p + h * kPLd + q4);
+      prow[0] = pw[0];
+      prow[1] = pw[1];
+      __syncthreads();
+      if ((t & 31) == 0) {
+        sh.m[h] = m_new;
+        sh.l[h] = sh.l[h] * alpha + psum;
+        sh.alpha[h] = alpha;
+      }
+    }
+    __syncthreads();
+    dbg_stamp(dbk, 2);
+
+    // PV: O[16 x 512] += P[16 x 128] V[128 x 512]
+    float a4[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) a4[r] = sh.alpha[4 * kc + r];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[nt][r] *= a4[r];
+#pragma unroll
+    for (int ks = 0; ks < kTile / 32; ++ks) {
+      const uint4 pa = *reinterpret_cast<const uint4*>(sh.p + kr * kPLd + 32 * ks + 8 * kc);
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const uint4 vb = load_v_operand(sh.vt, 32 * ks, 64 * wv + 16 * nt, lane);
+        o[nt] = mfma_bf16(pa, vb, o[nt]);
+      }
+    }
+    __syncthreads();
+  }
+
+  dbg_stamp(dbk, 3);
+  // partials: O [16][512] (unnormalised), (m, l) per head, log2 domain
+  const long pblk0 = ((long)b * nhg + hg) * nsplit;
+  const long pblk = pblk0 + sp;
+  float* po = A.part_o + pblk * (kHG * DSA_LATENT_DIM);
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      store_dev(&po[(4 * kc + r) * DSA_LATENT_DIM + 64 * wv + 16 * nt + kr], o[nt][r]);
+  if (t < kHG) {
+    store_dev(&A.part_ml[pblk * (2 * kHG) + 2 * t], sh.m[t]);
+    store_dev(&A.part_ml[pblk * (2 * kHG) + 2 * t + 1], sh.l[t]);
+  }
+
+  // arrival: the partials went out with device-scope stores; wait for them,
+  // then count -- the last split of (row, head group) merges
+  wait_mem();
+  __syncthreads();
+  if (t == 0) {
+    const uint32_t prev = atomicAdd(&A.counters[(long)b * nhg + hg], 1u);
+    sh.last = (prev == (uint32_t)nsplit - 1u) ? 1u : 0u;
+  }
+  __syncthreads();
+  dbg_stamp(dbk, 4);
+  if (!sh.last) return;
+  if (t == 0) A.counters[(long)b * nhg + hg] = 0u;  // re-arm for the next call
+  dbg_stamp(dbk, 5);
+
+  // log-sum-exp merge (reference combine_kernel K:996-1045):
+  // m* = max m_s, L = sum l_s 2^(m_s - m*), out = sum O_s 2^(m_s - m*) / L.
+  // 16 heads x 512 dims = 2048 float4 outputs, 4 per thread: two rounds of
+  // 2 outputs x 16 splits of device-scope loads, the first round issued
+  // together with the (m, l) loads.
+  float* mls = reinterpret_cast<float*>(sh.vt);
+  float* wgt = mls + kMaxSplit * 2 * kHG;
+  const float* pbase = A.part_o + pblk0 * (kHG * DSA_LATENT_DIM);
+  const __amdgpu_buffer_rsrc_t prs = dev_rsrc(pbase, (uint32_t)nsplit * kHG * DSA_LATENT_DIM * 4u);
+  const __amdgpu_buffer_rsrc_t mrs = dev_rsrc(A.part_ml + pblk0 * 2 * kHG, nsplit * 2 * kHG * 4u);
+  constexpr int kMS = 16;              // splits per load round
+  constexpr int kOut = 2;              // float4 outputs per round
+  constexpr int kVec = kHG * DSA_LATENT_DIM / 4;
+  auto load_round = [&](float4 (&x)[kOut][kMS], int v0, int s0) {
+#pragma unroll
+    for (int o2 = 0; o2 < kOut; ++o2)
+#pragma unroll
+      for (int i = 0; i < kMS; ++i)
+        x[o2][i] = (s0 + i < nsplit)
+                       ? __builtin_bit_cast(float4, load_dev16(prs, 16u * ((s0 + i) * kVec + v0 + o2 * kMainThreads)))
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+  };
+  float4 x[kOut][kMS];
+  load_round(x, t, 0);
+  {  // nsplit*32 floats, <= 8 per thread
+    constexpr int kPer = kMaxSplit * 2 * kHG / kMainThreads;
+    float v[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = t + j * kMainThreads;
+      v[j] = (i < nsplit * 2 * kHG) ? __uint_as_float(load_dev4(mrs, 4u * i)) : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j)
+      if (t + j * kMainThreads < nsplit * 2 * kHG) mls[t + j * kMainThreads] = v[j];
+  }
+  __syncthreads();
+  if (t < kHG) {
+    const float* ml = mls + 2 * t;
+    float mx = -INFINITY;
+    for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, ml[s * 2 * kHG]);
+    float L = 0.f;
+    if (mx != -INFINITY)
+      for (int s = 0; s < nsplit; ++s) {
+        const float ms = ml[s * 2 * kHG];
+        if (ms != -INFINITY) L += ml[s * 2 * kHG + 1] * exp2f(ms - mx);
+      }
+    const float inv = (mx != -INFINITY && L > 0.f) ? 1.f / L : 0.f;
+    for (int s = 0; s < nsplit; ++s) {
+      const float ms = ml[s * 2 * kHG];
+      wgt[s * kHG + t] = (ms != -INFINITY) ? exp2f(ms - mx) * inv : 0.f;
+    }
+  }
+  __syncthreads();
+  dbg_stamp(dbk, 6);
+  for (int v0 = t; v0 < kVec; v0 += kOut * kMainThreads) {
+    float4 acc[kOut];
+#pragma unroll
+    for (int o2 = 0; o2 < kOut; ++o2) acc[o2] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = 0; s0 < nsplit; s0 += kMS) {
+      if (v0 != t || s0 != 0) load_round(x, v0, s0);
+#pragma unroll
+      for (int o2 = 0; o2 < kOut; ++o2) {
+        const int h = (v0 + o2 * kMainThreads) / (DSA_LATENT_DIM / 4);
+#pragma unroll
+        for (int i = 0; i < kMS; ++i) {
+          const float wt = (s0 + i < nsplit) ? wgt[(s0 + i) * kHG + h] : 0.f;
+          acc[o2].x += x[o2][i].x * wt; acc[o2].y += x[o2][i].y * wt;
+          acc[o2].z += x[o2][i].z * wt; acc[o2].w += x[o2][i].w * wt;
+        }
+      }
+    }
+#pragma unroll
+    for (int o2 = 0; o2 < kOut; ++o2) {
+      const int v = v0 + o2 * kMainThreads;
+      const int h = v / (DSA_LATENT_DIM / 4);
+      uint2 pk;
+      pk.x = pack_bf16x2(acc[o2].x, acc[o2].y);
+      pk.y = pack_bf16x2(acc[o2].z, acc[o2].w);
+      const int d = (v % (DSA_LATENT_DIM / 4)) * 4;
+      *reinterpret_cast<uint2*>(A.out + ((long)b * A.H + hg * kHG + h) * DSA_LATENT_DIM + d) = pk;
+    }
+  }
+  dbg_stamp(dbk, 7);
+}
+
+// ======================================================================
+// indexer-scan role
+// ======================================================================
+constexpr int kChunkKeys = 16;
+constexpr int kScanBatch = 8;  // chunks per wave with loads in flight
+constexpr int kHistBins = 4096;
+
+struct ScanShared {
+  uint8_t qs[64 * DSA_INDEX_DIM];
+  float ws[64];
+  uint32_t hist[kHistBins];
+};
+
+template <int VARIANT>
+__device__ __forceinline__ v4f qk_fp8(const v8i& qa, const v8i& kb) {
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (VARIANT == 0) {
+    acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(qa, kb, acc, 0, 0, 0, 0, 0, 0);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const long a = ((long)(uint32_t)qa[2 * j]) | ((long)(uint32_t)qa[2 * j + 1] << 32);
+      const long bb = ((long)(uint32_t)kb[2 * j]) | ((long)(uint32_t)kb[2 * j + 1] << 32);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(a, bb, acc, 0, 0, 0);
+    }
+  }
+  return acc;
+}
+
+template <int NHG, int VARIANT>
+__device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, unsigned char* smem) {
+  constexpr int kHeads = NHG * 16;
+  ScanShared& sh = *reinterpret_cast<ScanShared*>(smem);
+  const int t = threadIdx.x;
+  const bool with_hist = S.hist != nullptr;
+  const int dbk = blockIdx.x;
+  dbg_stamp(dbk, 0);
+  {
+    const uint4* src = reinterpret_cast<const uint4*>(S.q8 + (long)row * kHeads * DSA_INDEX_DIM);
+    for (int i = t; i < kHeads * DSA_INDEX_DIM / 16; i += kMainThreads)
+      reinterpret_cast<uint4*>(sh.qs)[i] = src[i];
+    if (t < kHeads) sh.ws[t] = S.w[(long)row * kHeads + t];
+    if (with_hist)
+      for (int i = t; i < kHistBins; i += kMainThreads) sh.hist[i] = 0u;
+  }
+  const int cap = min(S.slab_stride, S.pt_stride * DSA_PAGE_TOKENS);
+  const int len = max(0, min(S.seq_lens[row], cap));
+  const int nchunks = (len + kChunkKeys - 1) / kChunkKeys;
+  const int nb = S.blocks_per_row;
+  const int c0 = (int)((long)nchunks * bid / nb);
+  const int c1 = (int)((long)nchunks * (bid + 1) / nb);
+  float* srow = S.scores + (long)row * S.slab_stride;
+  {  // slab tail past the last scored chunk -> -inf, spread over the row's blocks
+    const long tail0 = (long)nchunks * kChunkKeys;
+    const long tail = (long)S.slab_stride - tail0;
+    if (tail > 0) {
+      const long p0 = tail0 + tail * bid / nb, p1 = tail0 + tail * (bid + 1) / nb;
+      for (long p = p0 + t; p < p1; p += kMainThreads) {
+        if (S.next_idx) store_dev(&srow[p], -INFINITY);
+        else srow[p] = -INFINITY;
+      }
+    }
+  }
+  __syncthreads();
+
+  dbg_stamp(dbk, 1);
+  const int lane = t & (kWave - 1);
+  const int wv = wave_id();
+  const int kr = lane & 15, kc = lane >> 4;
+  v8i qa[NHG];
+  float wr[NHG][4];
+#pragma unroll
+  for (int hg = 0; hg < NHG; ++hg) {
+    const uint4* p = reinterpret_cast<const uint4*>(sh.qs + (hg * 16 + kr) * DSA_INDEX_DIM + kc * 32);
+    const uint4 a = p[0], bq = p[1];
+    qa[hg] = v8i{(int)a.x, (int)a.y, (int)a.z, (int)a.w, (int)bq.x, (int)bq.y, (int)bq.z, (int)bq.w};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) wr[hg][r] = sh.ws[hg * 16 + 4 * kc + r];
+  }
+
+  const int n = c1 - c0;
+  const int w0 = c0 + (int)((long)n * wv / kMainWaves);
+  const int w1 = c0 + (int)((long)n * (wv + 1) / kMainWaves);
+  const int* pt_row = S.page_table + (long)row * S.pt_stride;
+  for (int cb = w0; cb < w1; cb += kScanBatch) {
+    uint4 kv[kScanBatch][2];
+    float ksc[kScanBatch];
+    bool ok[kScanBatch];
+    int page[kScanBatch];
+#pragma unroll
+    for (int i = 0; i < kScanBatch; ++i) page[i] = (cb + i < w1) ? pt_row[(cb + i) >> 2] : -1;
+#pragma unroll
+    for (int i = 0; i < kScanBatch; ++i) {
+      const int c = cb + i;
+      ok[i] = c < w1 && page[i] >= 0 && (long)page[i] < S.num_pages;
+      kv[i][0] = kv[i][1] = make_uint4(0, 0, 0, 0);
+      ksc[i] = 0.f;
+      if (ok[i]) {
+        const uint8_t* base = S.pages + (long)page[i] * DSA_INDEX_PAGE_BYTES;
+        const uint4* kp = reinterpret_cast<const uint4*>(
+            base + (c & 3) * (kChunkKeys * DSA_INDEX_DIM) + kr * DSA_INDEX_DIM + kc * 32);
+        kv[i][0] = kp[0];
+        kv[i][1] = kp[1];
+        ksc[i] = reinterpret_cast<const float*>(base + DSA_PAGE_TOKENS * DSA_INDEX_DIM)[(c & 3) * kChunkKeys + kr];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kScanBatch; ++i) {
+      const int c = cb + i;
+      if (c >= w1) break;
+      float acc = 0.f;
+      if (ok[i]) {
+        const v8i kb = v8i{(int)kv[i][0].x, (int)kv[i][0].y, (int)kv[i][0].z, (int)kv[i][0].w,
+                           (int)kv[i][1].x, (int)kv[i][1].y, (int)kv[i][1].z, (int)kv[i][1].w};
+#pragma unroll
+        for (int hg = 0; hg < NHG; ++hg) {
+          const v4f d = qk_fp8<VARIANT>(qa[hg], kb);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc += wr[hg][r] * fmaxf(d[r], 0.f);
+        }
+        acc += __shfl_xor(acc, 16);
+        acc += __shfl_xor(acc, 32);
+      }
+      const int g = c * kChunkKeys + kr;
+      if (lane < 16 && g < S.slab_stride) {
+        const float v = (ok[i] && g < len) ? acc * ksc[i] : -INFINITY;
+        // device-scope stores when the row's last workgroup reads them back
+        if (S.next_idx) store_dev(&srow[g], v);
+        else srow[g] = v;
+        if (with_hist && g < len) atomicAdd(&sh.hist[rank_key(v) >> 20], 1u);
+      }
+    }
+  }
+  dbg_stamp(dbk, 2);
+  if (!with_hist) return;
+  __syncthreads();
+  uint32_t* rs = S.hist + (long)row * S.hist_row_words;
+  for (int i = t; i < kHistBins; i += kMainThreads) {
+    const uint32_t c = sh.hist[i];
+    if (c) atomicAdd(&rs[i], c);
+  }
+  dbg_stamp(dbk, 3);
+  if (!S.next_idx) return;
+  // arrival: wait for this slice's device-scope score stores and histogram
+  // atomics, then count; the row's last slice selects
+  wait_mem();
+  __syncthreads();
+  __shared__ uint32_t last;
+  if (t == 0) last = (atomicAdd(&rs[kArrOff], 1u) == (uint32_t)nb - 1u) ? 1u : 0u;
+  __syncthreads();
+  if (!last) return;
+  if (t == 0) rs[kArrOff] = 0u;
+  dbg_stamp(dbk, 4);
+  FinShared& fs = *reinterpret_cast<FinShared*>(smem);  // the scan's LDS is dead now
+  finalize_row(fs, srow, len, pt_row, S.pt_stride, rs, S.next_idx + (long)row * S.topk,
+               S.slab_stride, S.topk, /*sorted=*/0, /*pad=*/-1, /*fused=*/true);
+  dbg_stamp(dbk, 5);
+}
+
+// ======================================================================
+// the fused launch
+// ======================================================================
+template <int NHG, int VARIANT>
+__global__ __launch_bounds__(kMainThreads) void decode_main_kernel(AttnArgs A, int n_att, ScanArgs S) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  int bid = blockIdx.x;
+  if (bid < n_att) {
+    const int nhg = A.H / kHG;
+    const int sp = bid % A.nsplit;
+    const int hg = (bid / A.nsplit) % nhg;
+    const int b = bid / (A.nsplit * nhg);
+    attention_block(A, b, hg, sp, smem);
+    return;
+  }
+  bid -= n_att;
+  const int row = bid / S.blocks_per_row;
+  scan_block<NHG, VARIANT>(S, row, bid % S.blocks_per_row, smem);
+}
+
+// ---------------------------------------------------------------- host side
+static int g_scan_variant = 0;
+void set_scan_variant(int v) { g_scan_variant = v ? 1 : 0; }
+
+static int device_cus() {
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0;
+    hipDeviceProp_t prop;
+    cus = (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess)
+              ? prop.multiProcessorCount
+              : 256;
+  }
+  return cus;
+}
+
+int attn_auto_nsplit(int topk) { return std::max(1, std::min(kMaxSplit, (topk + kTile - 1) / kTile)); }
+
+size_t attn_workspace_bytes(int B, int H, int nsplit) {
+  const size_t blocks = (size_t)B * (H / kHG) * nsplit;
+  const size_t counters = ((size_t)B * (H / kHG) + 63) / 64 * 64;
+  return (blocks * kHG * (DSA_LATENT_DIM + 2) + counters) * sizeof(float);
+}
+
+void attn_bind_workspace(AttnArgs& A, void* ws, int B) {
+  const size_t blocks = (size_t)B * (A.H / kHG) * A.nsplit;
+  A.part_o = reinterpret_cast<float*>(ws);
+  A.part_ml = A.part_o + blocks * kHG * DSA_LATENT_DIM;
+  A.counters = reinterpret_cast<uint32_t*>(A.part_ml + blocks * 2 * kHG);
+}
+
+int scan_blocks_per_row(int B, int pt_stride, int slab_stride, int att_blocks, bool big_lds) {
+  const long cap = std::min((long)slab_stride, (long)pt_stride * DSA_PAGE_TOKENS);
+  const long cap_chunks = (cap + kChunkKeys - 1) / kChunkKeys;
+  const int cus = device_cus();
+  // when the launch's LDS (attention tile or the select) pins one block per
+  // CU, fill the CUs the attention leaves; a plain scan: two blocks per CU
+  const long target = big_lds ? std::max<long>(cus - att_blocks, cus / 2) : 2L * cus;
+  long per_row = (target + B - 1) / B;
+  per_row = std::min(per_row, std::max(1L, cap_chunks / kMainWaves));
+  return (int)std::max(1L, per_row);
+}
+
+template <int NHG>
+static hipError_t launch_nhg(dim3 grid, size_t lds, hipStream_t s, const AttnArgs& A, int n_att,
+                             const ScanArgs& S) {
+  if (g_scan_variant == 0)
+    hipLaunchKernelGGL((decode_main_kernel<NHG, 0>), grid, dim3(kMainThreads), lds, s, A, n_att, S);
+  else
+    hipLaunchKernelGGL((decode_main_kernel<NHG, 1>), grid, dim3(kMainThreads), lds, s, A, n_att, S);
+  return hipGetLastError();
+}
+
+template <int NHG>
+static hipError_t set_lds_attr(size_t lds) {
+  hipError_t e = hipFuncSetAttribute((const void*)decode_main_kernel<NHG, 0>,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
+  return hipFuncSetAttribute((const void*)decode_main_kernel<NHG, 1>,
+                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+}
+
+hipError_t launch_decode_main(const AttnArgs* A, int B_att, const ScanArgs* S, int B_scan,
+                              hipStream_t s) {
+  static bool attr_set = false;
+  const size_t lds_attn = sizeof(AttnShared);
+  if (!attr_set) {
+    const size_t lds_max = std::max(lds_attn, row_select_lds_bytes());
+    hipError_t e;
+    if ((e = set_lds_attr<1>(lds_max)) != hipSuccess) return e;
+    if ((e = set_lds_attr<2>(lds_max)) != hipSuccess) return e;
+    if ((e = set_lds_attr<3>(lds_max)) != hipSuccess) return e;
+    if ((e = set_lds_attr<4>(lds_max)) != hipSuccess) return e;
+    attr_set = true;
+  }
+  AttnArgs a{};
+  ScanArgs sc{};
+  int n_att = 0, n_scan = 0;
+  if (A) {
+    a = *A;
+    n_att = B_att * (a.H / kHG) * a.nsplit;
+  }
+  const bool select = S && S->next_idx;
+  if (S) {
+    sc = *S;
+    sc.blocks_per_row = scan_blocks_per_row(B_scan, sc.pt_stride, sc.slab_stride, n_att,
+                                            n_att > 0 || select);
+    n_scan = B_scan * sc.blocks_per_row;
+  }
+  if (n_att + n_scan == 0) return hipSuccess;
+  size_t lds = sizeof(ScanShared);
+  if (n_att) lds = std::max(lds, lds_attn);
+  if (select) lds = std::max(lds, row_select_lds_bytes());
+  const dim3 grid(n_att + n_scan);
+  switch (S ? sc.Hidx / 16 : 4) {
+    case 1: return launch_nhg<1>(grid, lds, s, a, n_att, sc);
+    case 2: return launch_nhg<2>(grid, lds, s, a, n_att, sc);
+    case 3: return launch_nhg<3>(grid, lds, s, a, n_att, sc);
+    default: return launch_nhg<4>(grid, lds, s, a, n_att, sc);
+  }
+}
+
+}  // namespace dsa

@@ -68,4 +68,51 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// ---- device-coherent publication between workgroups of one launch ----
+// Data a workgroup hands to the "last arriving" workgroup of its group is
+// written with device-scope stores (global_store ... sc1: coherent across
+// all XCDs' L2s by themselves), the writer waits for its stores to complete
+// (s_waitcnt), then increments an arrival counter with a device-scope
+// atomic.  The last arriver reads the data with device-scope loads
+// (buffer_load ... sc1).  This is the release/acquire the AMDGPU memory
+// model implements for agent-scope atomics, without the whole-L2 writeback
+// and invalidate (buffer_wbl2 / buffer_inv) that a fence would add per
+// workgroup.
+__device__ __forceinline__ void store_dev(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_dev(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_dev(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// wait until every memory operation this thread issued has completed
+__device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }
+
+constexpr int kCpolSc1 = 16;  // buffer-load cache policy: device scope
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+// 16 bytes at byte offset off (0 beyond the resource's size), device scope
+__device__ __forceinline__ uint4 load_dev16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCpolSc1));
+}
+__device__ __forceinline__ uint32_t load_dev4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kCpolSc1);
+}
+
+// Phase timestamps for profiling (off unless enabled through the internal
+// dsa_internal_debug entry point): thread 0 of workgroup `blk` records the
+// 100 MHz constant clock at phase `ph`; one predicated load when off.
+// Counterpart of the reference's hp_dbg stamps (K:1076-1091).
+constexpr int kDbgBlocks = 512;
+constexpr int kDbgPhases = 16;
+extern __device__ int g_dbg_on;
+extern __device__ unsigned long long g_dbg[kDbgBlocks * kDbgPhases];
+__device__ __forceinline__ void dbg_stamp(int blk, int ph) {
+  if (g_dbg_on && threadIdx.x == 0 && blk < kDbgBlocks)
+    g_dbg[blk * kDbgPhases + ph] = __builtin_amdgcn_s_memrealtime();
+}
+
 }  // namespace dsa

@@ -1,0 +1,61 @@
+// Host-side launch interface between the kernel files and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace dsa {
+
+// Split-K sparse MLA over the fp8 latent pool (attention role).
+struct AttnArgs {
+  const uint16_t* q;     // [B, H, 576] bf16
+  const uint8_t* pool;   // [kv_rows, 656]
+  long kv_rows;
+  const int* idx;        // [B, topk] KV slots
+  float* part_o;         // [B, H/16, nsplit, 16, 512]
+  float* part_ml;        // [B, H/16, nsplit, 16, 2]
+  uint32_t* counters;    // [B, H/16] arrival counters, zero between calls
+  uint16_t* out;         // [B, H, 512] bf16
+  int H, topk, nsplit;
+  float sm_log2;         // sm_scale * log2(e)
+};
+
+// Lightning-indexer scan over the paged fp8 index-K cache (scan role).
+struct ScanArgs {
+  const uint8_t* q8;     // [B, Hidx, 128] e4m3
+  const float* w;        // [B, Hidx]
+  const uint8_t* pages;  // [num_pages, 8448]
+  long num_pages;
+  const int* page_table; // [B, pt_stride]
+  const int* seq_lens;   // [B]
+  float* scores;         // [B, slab_stride]
+  uint32_t* hist;        // top-k scratch rows (nullptr: no histogram)
+  long hist_row_words;
+  int* next_idx;         // [B, topk]: when set, the row's last scan workgroup
+                         // runs the whole top-k select (KV-slot output, -1 pad)
+  int topk;
+  int pt_stride, slab_stride, Hidx;
+  int blocks_per_row;    // filled by the launcher
+};
+
+// One grid with n attention blocks (A != nullptr, rows B_att) and scan blocks
+// (S != nullptr, rows B_scan).
+hipError_t launch_decode_main(const AttnArgs* A, int B_att, const ScanArgs* S, int B_scan,
+                              hipStream_t s);
+void set_scan_variant(int v);
+int attn_auto_nsplit(int topk);
+size_t attn_workspace_bytes(int B, int H, int nsplit);
+void attn_bind_workspace(AttnArgs& A, void* ws, int B);
+
+// Top-k: histogram (standalone) + select (filter, last arriver finalizes).
+size_t topk_scratch_bytes(int B, int slab);
+size_t row_select_lds_bytes();
+long topk_row_words(int slab);
+hipError_t launch_topk_hist(const float* scores, const int* seq_lens, void* scratch, int B,
+                            int slab, int K, hipStream_t s);
+hipError_t launch_topk_select(const float* scores, const int* seq_lens, const int* page_table,
+                              int pt_stride, void* scratch, int* out, int B, int slab, int K,
+                              int sorted, int pad, hipStream_t s);
+
+}  // namespace dsa

@@ -20,7 +20,7 @@ CSRC = ROOT_DIR / "csrc"
 INCLUDE = REPO_DIR / "include"
 LIB_DIR = PKG_DIR / "_lib"
 LIB_PATH = LIB_DIR / "libdsa_mli.so"
-SOURCES = ["indexer_scan.hip", "topk.hip", "sparse_mla.hip", "capi.hip"]
+SOURCES = ["libdsa_mli.hip"]
 ARCH = "gfx950"
 
 

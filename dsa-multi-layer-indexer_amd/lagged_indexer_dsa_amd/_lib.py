@@ -75,7 +75,7 @@ SIGNATURES = {
     "dsa_mli_graph_create": (_i32, [ctypes.POINTER(LayerArgs), _i32, _vp, ctypes.POINTER(_vp)]),
     "dsa_mli_graph_launch": (_i32, [_vp, _vp]),
     "dsa_mli_graph_destroy": (_i32, [_vp]),
-    "dsa_mli_run_eager": (_i32, [ctypes.POINTER(LayerArgs), _i32, _vp, _vp]),
+    "dsa_mli_run_eager": (_i32, [ctypes.POINTER(LayerArgs), _i32, _vp]),
 }
 
 

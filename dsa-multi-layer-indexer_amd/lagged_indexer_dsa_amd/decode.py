@@ -6,8 +6,8 @@ paged fp8 index-K cache, the fp8 latent KV pool, the attention query, the
 score slab, the selection and the attention output.  :class:`MLISchedule`
 runs a stack of layers under the Multi-layer Indexer lag -- layer i attends
 the selection of the last earlier indexing layer while layer i's own
-indexer runs on a second stream -- eagerly or as one captured hipGraph
-(C ABI ``dsa_mli_graph_*``).
+indexer scan runs in the same launch (role-decoupled workgroups) -- eagerly
+or as one captured hipGraph (C ABI ``dsa_mli_graph_*``).
 
 Reference: DSAModel.forward LAGGED_FUSED (model.py:109-136),
 DSALayer.fused_attention_and_indices (dsa_layer.py:173-192), the serving
@@ -124,16 +124,12 @@ class MLISchedule:
             self._args.append(layer.args(att, indexer=indexer, attention=attention))
         self._arr = _arg_array(self._args)
         self._graph = None
-        self._side = None
 
     def run_eager(self) -> None:
-        if self._side is None:
-            self._side = torch.cuda.Stream()
-        main = torch.cuda.current_stream()
-        # side-stream buffers are used across the fork: hold refs (allocator
-        # safety, as P:2986-2990 does) -- the layers own them for our lifetime
-        _lib.call("dsa_mli_run_eager", self._arr, len(self._args), main.cuda_stream,
-                  self._side.cuda_stream)
+        # every buffer the launches touch is owned by the layers, which this
+        # schedule keeps alive (the allocator-safety rule of P:2986-2990)
+        _lib.call("dsa_mli_run_eager", self._arr, len(self._args),
+                  torch.cuda.current_stream().cuda_stream)
 
     def capture(self) -> None:
         """Capture the whole step into one hipGraph (two streams inside)."""

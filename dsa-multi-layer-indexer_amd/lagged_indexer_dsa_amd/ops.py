@@ -110,10 +110,12 @@ def topk(scores: torch.Tensor, seq_lens: torch.Tensor, k: int, sorted: bool = Fa
 
 
 def sparse_mla_workspace(B: int, H: int, nsplit: int, device) -> torch.Tensor:
+    """Zero-filled workspace (split partials + arrival counters; every call
+    leaves the counters zero)."""
     nbytes = _lib.load().dsa_sparse_mla_workspace_bytes(B, H, nsplit)
     if nbytes == 0:
         raise RuntimeError(f"bad sparse MLA workspace shape B={B} H={H} nsplit={nsplit}")
-    return torch.empty(nbytes // 4, dtype=torch.float32, device=device)
+    return torch.zeros(nbytes // 4, dtype=torch.float32, device=device)
 
 
 def sparse_mla_decode(q: torch.Tensor, kv_pool: torch.Tensor, idx: torch.Tensor,

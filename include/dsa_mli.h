@@ -116,12 +116,17 @@ int dsa_topk(const float* scores, const int32_t* seq_lens,
  *   out[b,h,:] = sum_j softmax_j(sm_scale * q[b,h,:] . kv_j) * kv_j[:512]
  * over the j in idx[b, :topk] with 0 <= idx < kv_rows (others are masked);
  * kv_j = dequant(row idx[b,j]) = bf16_rn(f32(e4m3) * scale[d/128]) for d<512,
- * rope bf16 for d>=512.  A row with no valid index gives 0.
- *   q        [B, H, 576] bf16;     kv_pool [kv_rows, 656] bytes
- *   idx      [B, topk] int32 KV slots
- *   part_o   workspace, dsa_sparse_mla_workspace_bytes() bytes
- *   out      [B, H, 512] bf16
- * H must be a multiple of 16; 1 <= nsplit <= 128 (nsplit=0: automatic).
+ * rope bf16 for d>=512.  A row with no valid index gives 0.  Indices are
+ * expected distinct (a repeated slot is counted once per occurrence).
+ *   q         [B, H, 576] bf16;     kv_pool [kv_rows, 656] bytes
+ *   idx       [B, topk] int32 KV slots
+ *   workspace dsa_sparse_mla_workspace_bytes(B, H, nsplit) bytes: split
+ *             partials plus per-(row, head group) arrival counters; zero-fill
+ *             it once before the first call, every call leaves the counters
+ *             zero again.  Calls that overlap in time must not share it.
+ *   out       [B, H, 512] bf16
+ * H must be a multiple of 16; 1 <= nsplit <= 128 (nsplit=0: automatic, and
+ * a workspace sized with nsplit=0 fits any nsplit).
  * Replaces: hp_attention_block + combine (K:1312-1666, K:996-1045) and
  * ref_sparse_mla (K:2950-2966); CPU semantics attention_core.py:94-146.
  */
@@ -133,9 +138,10 @@ int dsa_sparse_mla_decode(const void* q_bf16, const void* kv_pool,
 
 /*
  * (4) One DSA decode layer on one stream:
- *   scan -> top-k (position order, KV-slot output into next_idx) and
- *   attention over attend_idx (the lagged set), or over this layer's own
- *   fresh selection when attend_idx == NULL (baseline DSA).
+ *   indexer scan -> top-k (position order, KV-slot output into next_idx),
+ *   and attention over attend_idx (the lagged set: the attention and the
+ *   scan then share ONE launch), or over this layer's own fresh selection
+ *   when attend_idx == NULL (baseline DSA: scan, select, then attention).
  * scores [B, slab_stride] fp32 scratch; next_idx [B, topk] int32.
  * Replaces: DSALayer.fused_attention_and_indices (dsa_layer.py:173-192)
  * for one decode row per request.
@@ -149,12 +155,12 @@ typedef struct dsa_layer_args {
   float* scores;            /* [B, slab_stride] scratch */
   void* topk_scratch;       /* dsa_topk_scratch_bytes(B, slab_stride), zeroed once */
   int32_t* next_idx;        /* [B, topk] out: KV slots, -1 pad */
-  /* attention operands */
+  /* attention operands (NULL q_bf16: this layer runs no attention) */
   const void* q_bf16;       /* [B, H, 576] */
   const void* kv_pool;      /* [kv_rows, 656] */
   int64_t kv_rows;
-  const int32_t* attend_idx;/* [B, topk] KV slots; NULL = next_idx */
-  void* workspace;          /* dsa_sparse_mla_workspace_bytes(B,H,nsplit) */
+  const int32_t* attend_idx;/* [B, topk] KV slots; NULL = see (4) / (5) */
+  void* workspace;          /* dsa_sparse_mla_workspace_bytes(B,H,nsplit), zeroed once */
   void* out_bf16;           /* [B, H, 512] */
   /* shared */
   const int32_t* page_table;/* [B, pt_stride] */
@@ -166,15 +172,14 @@ typedef struct dsa_layer_args {
 int dsa_decode_layer(const dsa_layer_args* args, void* stream);
 
 /*
- * (5) MLI lag schedule as one hipGraph.  Layer i's attention runs on the
- * main stream over the set it is given; layer i's indexer (scan + top-k)
- * runs concurrently on a second stream and its selection is joined at the
- * entry of layer i+1's attention.  Layer i+1's indexer waits for layer i's
- * attention (its query derives from layer i+1's input).  attend_idx of a
- * layer that is NULL means "the selection produced most recently by an
- * earlier layer of the graph" (IndexCache reuse + lag); the first layer
- * must be given an explicit attend_idx.  A layer whose q_fp8 is NULL runs
- * no indexer.
+ * (5) MLI lag schedule over a stack of layers, eagerly or as one hipGraph.
+ * Layer i attends the selection of the most recent earlier layer that runs
+ * an indexer (its attend_idx when given; layer 0 must be given one), and
+ * layer i's indexer scan runs in the SAME launch as layer i's attention
+ * (role-decoupled workgroups), followed by layer i's top-k select, which
+ * layer i+1 attends.  A layer whose q_fp8 is NULL runs no indexer (IndexCache
+ * reuse); one whose q_bf16 is NULL runs no attention.  Everything is on one
+ * stream: the overlap of indexer and attention is inside each launch.
  * Replaces: DSAModel.forward LAGGED_FUSED (model.py:109-136) and the serving
  * side-stream fork/join (sglang overlay patch P:1774-1833, P:2942-2997).
  */
@@ -183,14 +188,8 @@ int dsa_mli_graph_create(const dsa_layer_args* layers, int num_layers,
                          void* capture_stream, dsa_mli_graph** out_graph);
 int dsa_mli_graph_launch(dsa_mli_graph* graph, void* stream);
 int dsa_mli_graph_destroy(dsa_mli_graph* graph);
-
-/*
- * Same schedule as dsa_mli_graph, enqueued eagerly (no graph): attention on
- * `stream`, indexers on `side_stream` (a different stream of the same
- * device), with event fork/join between them.  Returns once enqueued.
- */
 int dsa_mli_run_eager(const dsa_layer_args* layers, int num_layers,
-                      void* stream, void* side_stream);
+                      void* stream);
 
 #ifdef __cplusplus
 }

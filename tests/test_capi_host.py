@@ -105,8 +105,8 @@ def test_mla_contract_and_workspace(lib):
     assert f(16, 16, 0, 16, 16, 16, 1, 16, 2048, 0, 0.04, None) == DSA_ERR_INVALID_ARG
     assert f(None, 16, 10, 16, 16, 16, 1, 16, 2048, 0, 0.04, None) == DSA_ERR_INVALID_ARG
     ws = lib.dsa_sparse_mla_workspace_bytes
-    assert ws(1, 16, 32) == 32 * 16 * 514 * 4
-    assert ws(2, 32, 8) == 2 * 2 * 8 * 16 * 514 * 4
+    assert ws(1, 16, 32) == 32 * 16 * 514 * 4 + 64 * 4          # partials + counters
+    assert ws(2, 32, 8) == 2 * 2 * 8 * 16 * 514 * 4 + 64 * 4
     assert ws(1, 16, 0) == ws(1, 16, 128)
     assert ws(1, 15, 8) == 0
 
@@ -124,6 +124,6 @@ def test_mli_contract(lib):
     arr[0].out_bf16 = 16
     arr[0].B, arr[0].H, arr[0].topk = 1, 16, 2048
     assert lib.dsa_mli_graph_create(arr, 1, None, ctypes.byref(h)) == DSA_ERR_INVALID_ARG
-    assert lib.dsa_mli_run_eager(arr, 1, 16, 32) == DSA_ERR_INVALID_ARG
+    assert lib.dsa_mli_run_eager(arr, 1, 16) == DSA_ERR_INVALID_ARG
     assert lib.dsa_mli_graph_create(arr, 0, None, ctypes.byref(h)) == DSA_ERR_INVALID_ARG
     assert lib.dsa_mli_graph_destroy(None) == 0
