@@ -355,3 +355,11 @@ int dsa_internal_set_scan_variant(int v) {
 }
 
 }  // extern "C"
+// Internal: choose the cooperative (1, default) or single-workgroup (0)
+// select inside the decode launch; read (and optionally reset) the count of
+// group waits that expired.
+extern "C" int dsa_internal_set_coop_select(int on) {
+  dsa::set_coop_select(on);
+  return DSA_OK;
+}
+extern "C" int dsa_internal_group_wait_timeouts(int reset) { return dsa::group_wait_timeouts(reset); }

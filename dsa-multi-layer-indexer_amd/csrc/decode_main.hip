@@ -378,6 +378,178 @@ struct ScanShared {
   uint32_t hist[kHistBins];
 };
 
+// Cooperative select: the scan workgroup keeps the rank keys of its own
+// positions and takes part in the row's selection.
+constexpr int kCoopKeys = 16384;     // positions per workgroup
+constexpr int kCoopMaxBlocks = 256;  // workgroups per row
+struct CoopShared {
+  ScanShared scan;
+  uint32_t keys[kCoopKeys];
+  uint32_t cand_key[kCandCap];
+  int cand_idx[kCandCap];
+  uint32_t gts[kCoopMaxBlocks];
+  uint32_t wave_tmp[4 * kMainWaves];
+  uint32_t res[2];
+  uint32_t misc[4];
+  uint32_t sense[2];
+};
+
+// Row-wide exact top-k by all nb scan workgroups of the row (co-resident:
+// the launcher guarantees nb fits the device), each holding the keys of its
+// contiguous positions [p_lo, p_hi):
+//   barrier 1 (histogram complete) -> every workgroup derives the threshold
+//     bin T1, counts its finite keys above T1 and appends its bin-T1 keys to
+//     the row's candidate list;
+//   barrier 2 (counts and candidates complete) -> every workgroup refines
+//     the exact threshold key t* from the candidates (same result in each),
+//     computes its output offset from the counts of the workgroups before it
+//     and the candidates before p_lo, and writes its own selected positions
+//     (KV slots) in position order; ties at t* go to the lowest positions.
+// A candidate list that would overflow (more than kCandCap keys in bin T1,
+// e.g. many equal scores) hands the row to the single-workgroup select
+// instead.  The last workgroup to finish re-arms the row's scratch.
+__device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem, const ScanArgs& S, int bid,
+                                            int nb, int len, int p_lo, int p_hi, uint32_t* rs,
+                                            const float* srow, const int* pt_row, int* o) {
+  const int t = threadIdx.x;
+  const int K = S.topk;
+  const bool all = len <= K;
+  const int nown = max(0, p_hi - p_lo);
+  uint32_t* gcount = rs + kBmOff;                               // [nb]
+  uint32_t* gcand = rs + kBmOff + bitmap_words(S.slab_stride);  // keys [cap], positions [cap]
+  uint32_t* sync = rs + row_sync_off(S.slab_stride);             // barriers 1, 2
+  const int dbk = blockIdx.x;
+
+  uint32_t T1 = 0, above = 0, in_bin = 0;
+  if (!all) {
+    group_barrier(sync, bid, nb, cs.sense[0]);
+    dbg_stamp(dbk, 8);
+    copy_words_to_lds<kNB1 / 4 / kMainThreads, true>(cs.scan.hist, rs + kHistOff, kNB1);
+    __syncthreads();
+    find_threshold(cs.scan.hist, kNB1, (uint32_t)K, cs.wave_tmp, cs.res);
+    T1 = cs.res[0];
+    above = cs.res[1];
+    in_bin = cs.scan.hist[T1];
+    dbg_stamp(dbk, 9);
+  }
+  if (in_bin > (uint32_t)kCandCap) {
+    // single-workgroup fallback (it re-arms the histogram and count)
+    if (bid != nb - 1) return;
+    __syncthreads();
+    FinShared& fs = *reinterpret_cast<FinShared*>(smem);
+    finalize_row(fs, srow, len, pt_row, S.pt_stride, rs, o, S.slab_stride, K, 0, -1, /*fused=*/true);
+    return;
+  }
+
+  // ---- filter own positions: count, collect bin-T1 candidates ----
+  if (t == 0) cs.misc[0] = 0u;
+  __syncthreads();
+  uint32_t gt = 0;
+  for (int i = t; i < nown; i += kMainThreads) {
+    const uint32_t k = cs.keys[i];
+    const uint32_t bin = k >> 20;
+    const bool fin = key_is_finite(k);
+    if (all) {
+      gt += fin;
+    } else {
+      gt += (bin > T1 && fin) ? 1u : 0u;
+      if (bin == T1) {
+        const uint32_t slot = atomicAdd(&cs.misc[0], 1u);
+        cs.cand_key[slot] = k;
+        cs.cand_idx[slot] = p_lo + i;
+      }
+    }
+  }
+  const uint4 red = block_sum4(make_uint4(gt, 0, 0, 0), cs.wave_tmp);
+  if (t == 0) {
+    const uint32_t nmine = cs.misc[0];
+    cs.misc[1] = nmine ? atomicAdd(&rs[kCntOff], nmine) : 0u;
+    store_dev(&gcount[bid], red.x);
+  }
+  __syncthreads();
+  {
+    const uint32_t nmine = cs.misc[0], base = cs.misc[1];
+    for (uint32_t i = t; i < nmine; i += kMainThreads) {
+      store_dev(&gcand[base + i], cs.cand_key[i]);
+      store_dev(&gcand[kCandCap + base + i], (uint32_t)cs.cand_idx[i]);
+    }
+  }
+  group_barrier(sync + kSyncWords, bid, nb, cs.sense[1]);
+  dbg_stamp(dbk, 10);
+
+  // ---- every workgroup: candidates, counts, exact threshold ----
+  const int nc = (int)in_bin;
+  if (!all) {
+    copy_words_to_lds<kCandCap / 4 / kMainThreads, true>(cs.cand_key, gcand, nc);
+    copy_words_to_lds<kCandCap / 4 / kMainThreads, true>(reinterpret_cast<uint32_t*>(cs.cand_idx),
+                                                          gcand + kCandCap, nc);
+  }
+  copy_words_to_lds<kCoopMaxBlocks / 4 / kMainThreads + 1, true>(cs.gts, gcount, nb);
+  for (int i = t; i < kNB2; i += kMainThreads) cs.scan.hist[i] = 0u;
+  __syncthreads();
+  uint32_t tstar = 0, need3 = 0;
+  if (!all)
+    refine_candidates(cs.cand_key, nc, T1, (uint32_t)K - above, cs.scan.hist, cs.wave_tmp, cs.res,
+                      tstar, need3);
+  const bool tfin = !all && key_is_finite(tstar);
+  // x: counts of workgroups before this one, y: all counts,
+  // z: candidates above t* before p_lo, w: ties before p_lo; then above t* in all
+  uint4 acc = make_uint4(0, 0, 0, 0);
+  uint32_t c_gt_all = 0;
+  if (t < nb) {
+    const uint32_t c = cs.gts[t];
+    acc.x = (t < bid) ? c : 0u;
+    acc.y = c;
+  }
+  for (int j = t; j < nc; j += kMainThreads) {
+    const uint32_t k = cs.cand_key[j];
+    const bool g = k > tstar && key_is_finite(k);
+    const bool before = cs.cand_idx[j] < p_lo;
+    acc.z += (g && before) ? 1u : 0u;
+    acc.w += (k == tstar && before) ? 1u : 0u;
+    c_gt_all += g ? 1u : 0u;
+  }
+  const uint4 r1 = block_sum4(acc, cs.wave_tmp);
+  const uint4 r2 = block_sum4(make_uint4(c_gt_all, 0, 0, 0), cs.wave_tmp);
+  const uint32_t ties_before = r1.w;
+  const uint32_t base = r1.x + r1.z + (tfin ? min(ties_before, need3) : 0u);
+  const uint32_t nsel = r1.y + r2.x + (tfin ? need3 : 0u);
+  dbg_stamp(dbk, 11);
+
+  // ---- emit own selections in position order ----
+  uint32_t run_sel = 0, run_tie = ties_before;
+  for (int i0 = 0; i0 < nown; i0 += kMainThreads) {
+    const int i = i0 + t;
+    const bool in = i < nown;
+    const uint32_t k = in ? cs.keys[i] : 0u;
+    const bool tie = in && tfin && k == tstar;
+    uint32_t tie_tot, sel_tot;
+    const uint32_t tie_pre = block_flag_scan(tie, cs.wave_tmp, &tie_tot);
+    bool sel;
+    if (all) {
+      sel = in && key_is_finite(k);
+    } else {
+      const uint32_t bin = k >> 20;
+      sel = in && key_is_finite(k) &&
+            (bin > T1 || (bin == T1 && (k > tstar || (tie && run_tie + tie_pre < need3))));
+    }
+    const uint32_t sel_pre = block_flag_scan(sel, cs.wave_tmp, &sel_tot);
+    if (sel) {
+      const int p = p_lo + i;
+      o[base + run_sel + sel_pre] = pt_row[p >> 6] * DSA_PAGE_TOKENS + (p & (DSA_PAGE_TOKENS - 1));
+    }
+    run_sel += sel_tot;
+    run_tie += tie_tot;
+  }
+  if (bid == nb - 1)
+    for (int j = (int)nsel + t; j < K; j += kMainThreads) o[j] = -1;
+
+  // ---- re-arm: everyone has read the histogram (barrier 2 passed) ----
+  for (int i = kNB1 * bid / nb + t; i < kNB1 * (bid + 1) / nb; i += kMainThreads) rs[kHistOff + i] = 0u;
+  if (bid == 0 && t == 0) rs[kCntOff] = 0u;
+  dbg_stamp(dbk, 12);
+}
+
 template <int VARIANT>
 __device__ __forceinline__ v4f qk_fp8(const v8i& qa, const v8i& kb) {
   v4f acc = {0.f, 0.f, 0.f, 0.f};
@@ -409,6 +581,10 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
     if (t < kHeads) sh.ws[t] = S.w[(long)row * kHeads + t];
     if (with_hist)
       for (int i = t; i < kHistBins; i += kMainThreads) sh.hist[i] = 0u;
+    if (S.coop && t < kNumSync) {  // barrier senses: flipped once per use
+      const uint32_t* sync = S.hist + (long)row * S.hist_row_words + row_sync_off(S.slab_stride);
+      reinterpret_cast<CoopShared*>(smem)->sense[t] = group_sense(sync + t * kSyncWords, bid);
+    }
   }
   const int cap = min(S.slab_stride, S.pt_stride * DSA_PAGE_TOKENS);
   const int len = max(0, min(S.seq_lens[row], cap));
@@ -494,7 +670,11 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
         // device-scope stores when the row's last workgroup reads them back
         if (S.next_idx) store_dev(&srow[g], v);
         else srow[g] = v;
-        if (with_hist && g < len) atomicAdd(&sh.hist[rank_key(v) >> 20], 1u);
+        if (with_hist && g < len) {
+          const uint32_t key = rank_key(v);
+          atomicAdd(&sh.hist[key >> 20], 1u);
+          if (S.coop) reinterpret_cast<CoopShared*>(smem)->keys[g - c0 * kChunkKeys] = key;
+        }
       }
     }
   }
@@ -508,6 +688,11 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   }
   dbg_stamp(dbk, 3);
   if (!S.next_idx) return;
+  if (S.coop) {
+    coop_select(*reinterpret_cast<CoopShared*>(smem), smem, S, bid, nb, len, c0 * kChunkKeys,
+                min(c1 * kChunkKeys, len), rs, srow, pt_row, S.next_idx + (long)row * S.topk);
+    return;
+  }
   // arrival: wait for this slice's device-scope score stores and histogram
   // atomics, then count; the row's last slice selects
   wait_mem();
@@ -547,6 +732,17 @@ __global__ __launch_bounds__(kMainThreads) void decode_main_kernel(AttnArgs A, i
 // ---------------------------------------------------------------- host side
 static int g_scan_variant = 0;
 void set_scan_variant(int v) { g_scan_variant = v ? 1 : 0; }
+static int g_coop_select = 1;
+void set_coop_select(int on) { g_coop_select = on ? 1 : 0; }
+int group_wait_timeouts(int reset) {
+  int v = 0;
+  if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_group_wait_timeouts), sizeof(int)) != hipSuccess) return -1;
+  if (reset) {
+    const int z = 0;
+    if (hipMemcpyToSymbol(HIP_SYMBOL(g_group_wait_timeouts), &z, sizeof(int)) != hipSuccess) return -1;
+  }
+  return v;
+}
 
 static int device_cus() {
   static int cus = 0;
@@ -610,8 +806,9 @@ hipError_t launch_decode_main(const AttnArgs* A, int B_att, const ScanArgs* S, i
                               hipStream_t s) {
   static bool attr_set = false;
   const size_t lds_attn = sizeof(AttnShared);
+  const size_t lds_coop = std::max(sizeof(CoopShared), row_select_lds_bytes());
   if (!attr_set) {
-    const size_t lds_max = std::max(lds_attn, row_select_lds_bytes());
+    const size_t lds_max = std::max(lds_attn, lds_coop);
     hipError_t e;
     if ((e = set_lds_attr<1>(lds_max)) != hipSuccess) return e;
     if ((e = set_lds_attr<2>(lds_max)) != hipSuccess) return e;
@@ -631,12 +828,30 @@ hipError_t launch_decode_main(const AttnArgs* A, int B_att, const ScanArgs* S, i
     sc = *S;
     sc.blocks_per_row = scan_blocks_per_row(B_scan, sc.pt_stride, sc.slab_stride, n_att,
                                             n_att > 0 || select);
+    sc.coop = 0;
+    if (select && g_coop_select) {
+      // cooperative select: the row's workgroups wait for each other, so
+      // they must all be resident at once.  Workgroups are dispatched in
+      // index order, round-robin over the XCDs, and attention workgroups
+      // never wait: a row of at most (CUs - one per XCD) workgroups always
+      // becomes fully resident.  Each workgroup keeps its keys in LDS.
+      const long cap = std::min((long)sc.slab_stride, (long)sc.pt_stride * DSA_PAGE_TOKENS);
+      const long cap_chunks = (cap + kChunkKeys - 1) / kChunkKeys;
+      const long min_nb = (cap_chunks + kCoopKeys / kChunkKeys - 1) / (kCoopKeys / kChunkKeys);
+      const long max_nb = std::min<long>(kCoopMaxBlocks, device_cus() - 8);
+      const long bw = bitmap_words(sc.slab_stride);
+      long nb = std::max<long>(sc.blocks_per_row, min_nb);
+      if (nb <= max_nb && nb <= bw) {
+        sc.blocks_per_row = (int)nb;
+        sc.coop = 1;
+      }
+    }
     n_scan = B_scan * sc.blocks_per_row;
   }
   if (n_att + n_scan == 0) return hipSuccess;
   size_t lds = sizeof(ScanShared);
   if (n_att) lds = std::max(lds, lds_attn);
-  if (select) lds = std::max(lds, row_select_lds_bytes());
+  if (select) lds = std::max(lds, sc.coop ? lds_coop : row_select_lds_bytes());
   const dim3 grid(n_att + n_scan);
   switch (S ? sc.Hidx / 16 : 4) {
     case 1: return launch_nhg<1>(grid, lds, s, a, n_att, sc);

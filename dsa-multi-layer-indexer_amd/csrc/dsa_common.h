@@ -102,6 +102,94 @@ __device__ __forceinline__ uint32_t load_dev4(__amdgpu_buffer_rsrc_t r, uint32_t
   return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kCpolSc1);
 }
 
+// Sense-reversing group barrier between co-resident workgroups of one
+// launch.  sync: kGroupSyncGroups arrival counters, a top counter and
+// kGroupSyncFlags release flags, one 256-byte line each (zero before first
+// use).  Every member publishes (device-scope stores, waited for) and
+// arrives on its group's counter (member bid -> group bid % 16, so each line
+// sees few atomics); the last of a group arrives on the top counter; the
+// last of all re-zeroes the counters and flips the flags.  The others spin
+// on the flag of their XCD (bid % 8), reading it with device-scope loads.
+// `sense` is the flags' value before this barrier (read at launch start;
+// the flags flip once per use).  The wait is bounded (about a second): on
+// expiry it counts in g_group_wait_timeouts and goes on, so a launch that
+// breaks the co-residency assumption returns (with wrong results, and the
+// counter says so) instead of hanging the device.
+extern __device__ int g_group_wait_timeouts;
+constexpr int kGroupSpinMax = 1 << 20;
+constexpr int kGroupSyncGroups = 16, kGroupSyncFlags = 8, kGroupSyncLine = 64;
+__device__ __forceinline__ uint32_t group_sense(const uint32_t* sync, int bid) {
+  return __hip_atomic_load(&sync[(kGroupSyncGroups + 1 + (bid & (kGroupSyncFlags - 1))) * kGroupSyncLine],
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void group_barrier(uint32_t* sync, int bid, int nb, uint32_t sense) {
+  wait_mem();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int g = bid % kGroupSyncGroups;
+    const uint32_t ng = (uint32_t)((nb - 1 - g) / kGroupSyncGroups + 1);
+    bool last = false;
+    if (atomicAdd(&sync[g * kGroupSyncLine], 1u) == ng - 1u) {
+      const uint32_t ngroups = (uint32_t)min(nb, kGroupSyncGroups);
+      last = atomicAdd(&sync[kGroupSyncGroups * kGroupSyncLine], 1u) == ngroups - 1u;
+    }
+    if (last) {
+      for (int i = 0; i <= kGroupSyncGroups; ++i) store_dev(&sync[i * kGroupSyncLine], 0u);
+      wait_mem();
+      for (int f = 0; f < kGroupSyncFlags; ++f)
+        store_dev(&sync[(kGroupSyncGroups + 1 + f) * kGroupSyncLine], sense ^ 1u);
+    } else {
+      for (int i = 0; group_sense(sync, bid) == sense; ++i) {
+        if (i == kGroupSpinMax) {
+          atomicAdd(&g_group_wait_timeouts, 1);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// Exclusive prefix count of a per-thread flag in thread order; *total gets
+// the block's count.  wave_tmp: one word per wave.
+__device__ __forceinline__ uint32_t block_flag_scan(bool f, uint32_t* wave_tmp, uint32_t* total) {
+  const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave, nw = blockDim.x / kWave;
+  const uint64_t m = __ballot(f);
+  const uint32_t in_wave = (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
+  if (lane == 0) wave_tmp[wv] = (uint32_t)__popcll(m);
+  __syncthreads();
+  uint32_t before = 0, tot = 0;
+  for (int i = 0; i < nw; ++i) {
+    const uint32_t x = wave_tmp[i];
+    before += (i < wv) ? x : 0u;
+    tot += x;
+  }
+  __syncthreads();
+  *total = tot;
+  return before + in_wave;
+}
+
+// Block-wide sums of four per-thread counts.  wave_tmp: 4 words per wave.
+__device__ __forceinline__ uint4 block_sum4(uint4 v, uint32_t* wave_tmp) {
+  const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave, nw = blockDim.x / kWave;
+  for (int o = 32; o >= 1; o >>= 1) {
+    v.x += __shfl_xor(v.x, o);
+    v.y += __shfl_xor(v.y, o);
+    v.z += __shfl_xor(v.z, o);
+    v.w += __shfl_xor(v.w, o);
+  }
+  if (lane == 0) *reinterpret_cast<uint4*>(&wave_tmp[4 * wv]) = v;
+  __syncthreads();
+  uint4 r = make_uint4(0, 0, 0, 0);
+  for (int i = 0; i < nw; ++i) {
+    const uint4 x = *reinterpret_cast<const uint4*>(&wave_tmp[4 * i]);
+    r.x += x.x; r.y += x.y; r.z += x.z; r.w += x.w;
+  }
+  __syncthreads();
+  return r;
+}
+
 // Phase timestamps for profiling (off unless enabled through the internal
 // dsa_internal_debug entry point): thread 0 of workgroup `blk` records the
 // 100 MHz constant clock at phase `ph`; one predicated load when off.

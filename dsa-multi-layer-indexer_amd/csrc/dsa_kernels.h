@@ -37,6 +37,8 @@ struct ScanArgs {
   int topk;
   int pt_stride, slab_stride, Hidx;
   int blocks_per_row;    // filled by the launcher
+  int coop;              // filled by the launcher: the row's scan workgroups
+                         // select together (group barriers)
 };
 
 // One grid with n attention blocks (A != nullptr, rows B_att) and scan blocks
@@ -44,6 +46,8 @@ struct ScanArgs {
 hipError_t launch_decode_main(const AttnArgs* A, int B_att, const ScanArgs* S, int B_scan,
                               hipStream_t s);
 void set_scan_variant(int v);
+void set_coop_select(int on);
+int group_wait_timeouts(int reset);
 int attn_auto_nsplit(int topk);
 size_t attn_workspace_bytes(int B, int H, int nsplit);
 void attn_bind_workspace(AttnArgs& A, void* ws, int B);

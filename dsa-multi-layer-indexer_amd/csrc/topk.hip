@@ -36,6 +36,7 @@ namespace dsa {
 
 __device__ int g_dbg_on = 0;
 __device__ unsigned long long g_dbg[kDbgBlocks * kDbgPhases];
+__device__ int g_group_wait_timeouts = 0;
 
 constexpr int kNB1 = 4096;      // first digit: key bits [31:20]
 constexpr int kNB2 = 1024;      // refinements: bits [19:10], [9:0]
@@ -48,11 +49,25 @@ constexpr int kSlice = 4096;    // scores per slice workgroup (16 per thread)
 constexpr int kHistOff = 0;
 constexpr int kCntOff = kNB1;       // bin-T1 candidate count
 constexpr int kArrOff = kNB1 + 1;   // select workgroups arrived
+// cooperative select inside the decode launch (decode_main.hip): per-row
+// group barriers live after the candidates; per-workgroup counts in the
+// bitmap area, candidates (keys, then positions) in the candidate area
 constexpr int kBmOff = kNB1 + 64;
 
 __host__ __device__ inline long bitmap_words(int slab) { return ((long)slab + 2047) / 2048 * 64; }
+// group-barrier area (after the candidates): per barrier, kSyncGroups
+// arrival counters, one top counter and 8 release flags, each in its own
+// 256-byte line
+constexpr int kSyncGroups = 16;
+constexpr int kSyncFlags = 8;
+constexpr int kSyncLine = 64;  // words
+constexpr int kSyncWords = (kSyncGroups + 1 + kSyncFlags) * kSyncLine;
+constexpr int kNumSync = 2;
+static_assert(kSyncGroups == kGroupSyncGroups && kSyncFlags == kGroupSyncFlags && kSyncLine == kGroupSyncLine,
+              "group-barrier layout");
+__host__ __device__ inline long row_sync_off(int slab) { return kBmOff + bitmap_words(slab) + 2L * kCandCap; }
 __host__ __device__ inline long row_scratch_words(int slab) {
-  return kBmOff + bitmap_words(slab) + 2L * kCandCap;
+  return row_sync_off(slab) + (long)kNumSync * kSyncWords;
 }
 
 // Exclusive prefix sum over the block (thread order); *total gets the sum.
@@ -229,6 +244,35 @@ __device__ __forceinline__ void filter_slice(const float* __restrict__ s, int le
       slot0 += (uint32_t)__popcll(eqm[it]);
     }
   }
+}
+
+
+// Exact threshold key among the bin-T1 candidates ck[0..nc): two 10-bit
+// refinements (key bits [19:10], then [9:0]) of the `need1` keys still to
+// select.  tstar = the K-th ranked key, need3 = how many keys equal to it
+// are selected.  hist (>= kNB2 words of LDS) must be zero on entry and is
+// left dirty.
+__device__ __forceinline__ void refine_candidates(const uint32_t* ck, int nc, uint32_t T1, uint32_t need1,
+                                                  uint32_t* hist, uint32_t* wave_tmp, uint32_t* res,
+                                                  uint32_t& tstar, uint32_t& need3) {
+  const int t = threadIdx.x, nthr = blockDim.x;
+  for (int j = t; j < nc; j += nthr) atomicAdd(&hist[(ck[j] >> 10) & 1023u], 1u);
+  __syncthreads();
+  find_threshold(hist, kNB2, need1, wave_tmp, res);
+  const uint32_t T2 = res[0];
+  const uint32_t need2 = need1 - res[1];
+  __syncthreads();
+  for (int i = t; i < kNB2; i += nthr) hist[i] = 0u;
+  __syncthreads();
+  const uint32_t pre2 = (T1 << 10) | T2;
+  for (int j = t; j < nc; j += nthr) {
+    const uint32_t k = ck[j];
+    if ((k >> 10) == pre2) atomicAdd(&hist[k & 1023u], 1u);
+  }
+  __syncthreads();
+  find_threshold(hist, kNB2, need2, wave_tmp, res);
+  tstar = (pre2 << 10) | res[0];
+  need3 = need2 - res[1];
 }
 
 // ---------------------------------------------------------------- (C)
@@ -428,23 +472,7 @@ __device__ __forceinline__ void finalize_row(FinShared& sh, const float* __restr
         }
         __syncthreads();
       }
-      for (int j = t; j < nc; j += nthr) atomicAdd(&sh.hist[(sh.cand_key[j] >> 10) & 1023u], 1u);
-      __syncthreads();
-      find_threshold(sh.hist, kNB2, need1, sh.wave_tmp, sh.res);
-      const uint32_t T2 = sh.res[0];
-      const uint32_t need2 = need1 - sh.res[1];
-      __syncthreads();
-      for (int i = t; i < kNB2; i += nthr) sh.hist[i] = 0u;
-      __syncthreads();
-      const uint32_t pre2 = (T1 << 10) | T2;
-      for (int j = t; j < nc; j += nthr) {
-        const uint32_t k = sh.cand_key[j];
-        if ((k >> 10) == pre2) atomicAdd(&sh.hist[k & 1023u], 1u);
-      }
-      __syncthreads();
-      find_threshold(sh.hist, kNB2, need2, sh.wave_tmp, sh.res);
-      tstar = (pre2 << 10) | sh.res[0];
-      need3 = need2 - sh.res[1];
+      refine_candidates(sh.cand_key, nc, T1, need1, sh.hist, sh.wave_tmp, sh.res, tstar, need3);
       for (int j = t; j < nc; j += nthr) {
         const uint32_t k = sh.cand_key[j];
         if (k > tstar) {

@@ -96,6 +96,10 @@ def load(path: Path | None = None) -> ctypes.CDLL:
         fn.argtypes = args
     lib.dsa_internal_set_scan_variant.restype = _i32
     lib.dsa_internal_set_scan_variant.argtypes = [_i32]
+    lib.dsa_internal_set_coop_select.restype = _i32
+    lib.dsa_internal_set_coop_select.argtypes = [_i32]
+    lib.dsa_internal_group_wait_timeouts.restype = _i32
+    lib.dsa_internal_group_wait_timeouts.argtypes = [_i32]
     _LIB = lib
     return lib
 

@@ -1,0 +1,97 @@
+"""GPU: the top-k select fused into the decode launch's scan workgroups.
+
+The layer composite (scan + select in one launch, no attend set) must give
+the oracle's top-k of the scores it produced, mapped to KV slots, bit-exact
+(reference select_topk, attention_core.py:66-91, ties to the lower index).
+Covered: the cooperative select (all scan workgroups of a row; default) and
+the single-workgroup select, on ragged rows, rows of <= topk tokens, rows
+with many equal scores at the threshold, and rows whose threshold bin
+overflows the candidate list (every score equal).  No group wait may expire.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import dsa_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _lib():
+    from lagged_indexer_dsa_amd import _lib
+    return _lib.load()
+
+
+def _layer(dev, lens, seed, pattern=None):
+    from lagged_indexer_dsa_amd import synthetic as S
+
+    pt, num_pages = S.make_page_table(lens, seed=seed, device=dev)
+    L = S.make_decode_layer(lens, seed=seed + 1, device=dev, page_table=pt, num_pages=num_pages)
+    pages = L.index_k.view(num_pages, -1)
+    if pattern == "dup":      # every page repeats one of 8 pages: many equal scores
+        src = pages[:8].clone()
+        for p in range(num_pages):
+            pages[p] = src[p % 8]
+    elif pattern == "equal":  # every key and scale identical: all scores equal
+        pages[:, :8192] = pages[0, :128].repeat(64)
+        pages[:, 8192:].view(torch.float32).fill_(1.0)
+    return L, pt
+
+
+def _check(L, pt, lens):
+    torch.cuda.synchronize()
+    sc = L.scores.cpu().numpy()
+    ref = O.topk_select(sc, np.array(lens), L.topk, page_table=pt.cpu().numpy())
+    got = L.next_idx.cpu().numpy()
+    assert np.array_equal(got, ref), f"first mismatch rows {np.nonzero((got != ref).any(1))[0][:4]}"
+
+
+CASES = [
+    ([131072], 0, None),
+    ([5000, 3100, 70], 1, None),
+    ([2048, 2049, 1], 2, None),
+    ([20000, 9000], 3, "dup"),
+    ([6000, 4097], 4, "equal"),
+]
+
+
+@pytest.mark.parametrize("lens,seed,pattern", CASES)
+@pytest.mark.parametrize("coop", [1, 0])
+def test_fused_select_matches_oracle(dev, lens, seed, pattern, coop):
+    lib = _lib()
+    print(f"[fused-select] lens={lens} pattern={pattern} coop={coop}", flush=True)
+    lib.dsa_internal_group_wait_timeouts(1)
+    lib.dsa_internal_set_coop_select(coop)
+    try:
+        L, pt = _layer(dev, lens, 100 + seed, pattern)
+        for rep in range(3):  # the scratch re-arms itself between calls
+            L.next_idx.fill_(-7)
+            L.run(attend_idx=None)
+            _check(L, pt, lens)
+    finally:
+        lib.dsa_internal_set_coop_select(1)
+    assert lib.dsa_internal_group_wait_timeouts(1) == 0
+
+
+def test_fused_select_coop_equals_single(dev):
+    lib = _lib()
+    print("[fused-select] coop == single workgroup", flush=True)
+    lens = [70000, 1500, 33000]
+    L, pt = _layer(dev, lens, 7)
+    lib.dsa_internal_set_coop_select(0)
+    try:
+        L.run(attend_idx=None)
+        torch.cuda.synchronize()
+        single = L.next_idx.clone()
+        out_single = L.out.clone()
+    finally:
+        lib.dsa_internal_set_coop_select(1)
+    L.next_idx.fill_(-7)
+    L.run(attend_idx=None)
+    torch.cuda.synchronize()
+    assert torch.equal(single, L.next_idx)
+    assert torch.equal(out_single.view(torch.int16), L.out.view(torch.int16))
+    _check(L, pt, lens)
