@@ -372,31 +372,50 @@ constexpr int kChunkKeys = 16;
 constexpr int kScanBatch = 8;  // chunks per wave with loads in flight
 constexpr int kHistBins = 4096;
 
+constexpr int kScanMaxPages = 4100;  // page-table entries a workgroup prefetches
 struct ScanShared {
   uint8_t qs[64 * DSA_INDEX_DIM];
   float ws[64];
   uint32_t hist[kHistBins];
+  int pts[kScanMaxPages];
 };
 
 // Cooperative select: the scan workgroup keeps the rank keys of its own
 // positions and takes part in the row's selection.
-constexpr int kCoopKeys = 16384;     // positions per workgroup
+constexpr int kCoopKeys = 8192;      // positions per workgroup
 constexpr int kCoopMaxBlocks = 256;  // workgroups per row
+constexpr int kPubHdr = 4;           // published list: count, bound, finite count, -
 struct CoopShared {
   ScanShared scan;
   uint32_t keys[kCoopKeys];
-  uint32_t cand_key[kCandCap];
-  int cand_idx[kCandCap];
+  union {
+    struct {
+      uint32_t cand_key[kCandCap];
+      int cand_idx[kCandCap];
+    };
+    uint32_t pub[kPubWords];  // every workgroup's published list, stride pub_stride()
+  };
   uint32_t gts[kCoopMaxBlocks];
   uint32_t wave_tmp[4 * kMainWaves];
   uint32_t res[2];
   uint32_t misc[4];
-  uint32_t sense[2];
+  uint32_t sense[kNumSync];
 };
 
-// Row-wide exact top-k by all nb scan workgroups of the row (co-resident:
-// the launcher guarantees nb fits the device), each holding the keys of its
-// contiguous positions [p_lo, p_hi):
+// Words per workgroup in the published-key area (a multiple of 4): about
+// three times a workgroup's expected share of the K selected keys plus 16,
+// within the area.  A list too short for its workgroup only costs the
+// fallback to the histogram form.
+__host__ __device__ inline int pub_stride(int nb, int K) {
+  const int want = kPubHdr + 3 * ((K + nb - 1) / nb) + 16;
+  return min((want + 3) & ~3, (kPubWords / nb) & ~3);
+}
+
+// Histogram form of the cooperative select (the general case; the
+// published-list form below hands a row here when its lists cannot decide).
+// All nb scan workgroups of the row (co-resident: the launcher guarantees
+// nb fits the device), each holding the keys of its contiguous positions
+// [p_lo, p_hi), add their 12-bit key histograms to the row's, then:
 //   barrier 1 (histogram complete) -> every workgroup derives the threshold
 //     bin T1, counts its finite keys above T1 and appends its bin-T1 keys to
 //     the row's candidate list;
@@ -408,21 +427,31 @@ struct CoopShared {
 // A candidate list that would overflow (more than kCandCap keys in bin T1,
 // e.g. many equal scores) hands the row to the single-workgroup select
 // instead.  The last workgroup to finish re-arms the row's scratch.
-__device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem, const ScanArgs& S, int bid,
-                                            int nb, int len, int p_lo, int p_hi, uint32_t* rs,
-                                            const float* srow, const int* pt_row, int* o) {
+__device__ __forceinline__ void coop_select_hist(CoopShared& cs, unsigned char* smem, const ScanArgs& S,
+                                                 int bid, int nb, int len, int p_lo, int p_hi, uint32_t* rs,
+                                                 const float* srow, const int* pt_row, int* o) {
   const int t = threadIdx.x;
   const int K = S.topk;
   const bool all = len <= K;
   const int nown = max(0, p_hi - p_lo);
+  {  // this workgroup's histogram into the row's
+    for (int i = t; i < kNB1; i += kMainThreads) cs.scan.hist[i] = 0u;
+    __syncthreads();
+    for (int i = t; i < nown; i += kMainThreads) atomicAdd(&cs.scan.hist[cs.keys[i] >> 20], 1u);
+    __syncthreads();
+    for (int i = t; i < kNB1; i += kMainThreads) {
+      const uint32_t c = cs.scan.hist[i];
+      if (c) atomicAdd(&rs[kHistOff + i], c);
+    }
+  }
   uint32_t* gcount = rs + kBmOff;                               // [nb]
   uint32_t* gcand = rs + kBmOff + bitmap_words(S.slab_stride);  // keys [cap], positions [cap]
-  uint32_t* sync = rs + row_sync_off(S.slab_stride);             // barriers 1, 2
+  uint32_t* sync = rs + row_sync_off(S.slab_stride);             // barriers 0 (lists), 1, 2
   const int dbk = blockIdx.x;
 
   uint32_t T1 = 0, above = 0, in_bin = 0;
   if (!all) {
-    group_barrier(sync, bid, nb, cs.sense[0]);
+    group_barrier(sync + kSyncWords, bid, nb, cs.sense[1]);
     dbg_stamp(dbk, 8);
     copy_words_to_lds<kNB1 / 4 / kMainThreads, true>(cs.scan.hist, rs + kHistOff, kNB1);
     __syncthreads();
@@ -474,24 +503,46 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
       store_dev(&gcand[kCandCap + base + i], (uint32_t)cs.cand_idx[i]);
     }
   }
-  group_barrier(sync + kSyncWords, bid, nb, cs.sense[1]);
+  group_barrier(sync + 2 * kSyncWords, bid, nb, cs.sense[2]);
   dbg_stamp(dbk, 10);
 
   // ---- every workgroup: candidates, counts, exact threshold ----
   const int nc = (int)in_bin;
-  if (!all) {
-    copy_words_to_lds<kCandCap / 4 / kMainThreads, true>(cs.cand_key, gcand, nc);
-    copy_words_to_lds<kCandCap / 4 / kMainThreads, true>(reinterpret_cast<uint32_t*>(cs.cand_idx),
-                                                          gcand + kCandCap, nc);
+  {  // candidates (keys, positions) and the per-workgroup counts: one batch of loads
+    constexpr int kP = kCandCap / 4 / kMainThreads;
+    const __amdgpu_buffer_rsrc_t cr = dev_rsrc(gcand, 8u * kCandCap);
+    const __amdgpu_buffer_rsrc_t gr = dev_rsrc(gcount, 4u * (uint32_t)nb);
+    const int nc4 = all ? 0 : (nc + 3) >> 2;
+    uint4 ka[kP], ia[kP];
+    uint32_t gv = 0;
+#pragma unroll
+    for (int j = 0; j < kP; ++j) {
+      const int i = t + j * kMainThreads;
+      if (i < nc4) {
+        ka[j] = load_dev16(cr, 16u * i);
+        ia[j] = load_dev16(cr, 4u * kCandCap + 16u * i);
+      }
+    }
+    if (t < nb) gv = load_dev4(gr, 4u * t);
+#pragma unroll
+    for (int j = 0; j < kP; ++j) {
+      const int i = t + j * kMainThreads;
+      if (i < nc4) {
+        reinterpret_cast<uint4*>(cs.cand_key)[i] = ka[j];
+        reinterpret_cast<uint4*>(cs.cand_idx)[i] = ia[j];
+      }
+    }
+    if (t < nb) cs.gts[t] = gv;
   }
-  copy_words_to_lds<kCoopMaxBlocks / 4 / kMainThreads + 1, true>(cs.gts, gcount, nb);
   for (int i = t; i < kNB2; i += kMainThreads) cs.scan.hist[i] = 0u;
   __syncthreads();
+  dbg_stamp(dbk, 13);
   uint32_t tstar = 0, need3 = 0;
   if (!all)
     refine_candidates(cs.cand_key, nc, T1, (uint32_t)K - above, cs.scan.hist, cs.wave_tmp, cs.res,
                       tstar, need3);
   const bool tfin = !all && key_is_finite(tstar);
+  dbg_stamp(dbk, 14);
   // x: counts of workgroups before this one, y: all counts,
   // z: candidates above t* before p_lo, w: ties before p_lo; then above t* in all
   uint4 acc = make_uint4(0, 0, 0, 0);
@@ -550,6 +601,221 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
   dbg_stamp(dbk, 12);
 }
 
+// Published-list form of the cooperative select (the default).  Each scan
+// workgroup of the row publishes, in its stride of the row's list area,
+// every own key in the 12-bit bins >= its bound bin Bb (at most
+// M = stride - 4 keys; Bb = 0 when it holds at most M keys), zero-padded,
+// after a header {count, Bb, finite count} (header words and padding are
+// below every real key: the smallest, -inf, is 0x007fffff).  After ONE
+// group barrier every workgroup reads all lists and, from them alone,
+// finds the exact K-th key t* of their union and the ties to take.  The
+// union holds every key >= t* of the row exactly when t* >> 20 >= every
+// Bb; the workgroups check that (they all see the same lists, so they
+// agree) and otherwise hand the row to the histogram form.  The offsets
+// follow from the lists of the workgroups before this one; each workgroup
+// then writes its own selected positions (KV slots) in position order.
+__device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem, const ScanArgs& S, int bid,
+                                            int nb, int len, int p_lo, int p_hi, uint32_t* rs,
+                                            const float* srow, const int* pt_row, int* o) {
+  const int t = threadIdx.x;
+  const int K = S.topk;
+  const bool all = len <= K;
+  const int nown = max(0, p_hi - p_lo);
+  const int P = pub_stride(nb, K);
+  const uint32_t M = (uint32_t)(P - kPubHdr);
+  uint32_t* gpub = rs + row_pub_off(S.slab_stride);
+  uint32_t* sync = rs + row_sync_off(S.slab_stride);
+  const int dbk = blockIdx.x;
+
+  // ---- own list: every key in bins >= Bb ----
+  uint32_t Bb = 0;
+  if (all) {
+    Bb = kNB1;  // nothing to publish but the finite count
+  } else if ((uint32_t)nown > M) {
+    find_threshold_fixed<kNB1, kMainThreads>(cs.scan.hist, M, cs.wave_tmp, cs.res);  // own histogram
+    const uint32_t Tb = cs.res[0];
+    Bb = (cs.res[1] + cs.scan.hist[Tb] <= M) ? Tb : Tb + 1u;
+  }
+  if (t == 0) cs.misc[0] = 0u;
+  __syncthreads();
+  uint32_t nfin = 0;
+  for (int i = t; i < nown; i += kMainThreads) {
+    const uint32_t k = cs.keys[i];
+    nfin += key_is_finite(k) ? 1u : 0u;
+    if ((k >> 20) >= Bb) cs.pub[atomicAdd(&cs.misc[0], 1u)] = k;
+  }
+  const uint32_t fin_own = block_reduce4<0, 0, 0, 0>(make_uint4(nfin, 0, 0, 0), cs.wave_tmp).x;
+  {
+    const uint32_t cnt = cs.misc[0];
+    uint32_t* mine = gpub + (long)bid * P;
+    for (int i = t; i < P; i += kMainThreads) {
+      uint32_t v = 0u;
+      if (i == 0) v = cnt;
+      else if (i == 1) v = Bb;
+      else if (i == 2) v = fin_own;
+      else if (i >= kPubHdr && (uint32_t)(i - kPubHdr) < cnt) v = cs.pub[i - kPubHdr];
+      store_dev(&mine[i], v);
+    }
+  }
+  dbg_stamp(dbk, 8);
+  group_barrier(sync, bid, nb, cs.sense[0]);
+  dbg_stamp(dbk, 9);
+
+  // ---- every workgroup: all lists into LDS (one batch of device-scope
+  // loads), the headers' bounds and finite counts ----
+  const int nent = nb * P;
+  const int n4 = nent >> 2;
+  uint32_t hdr_b = 0, hdr_f = 0;
+  {
+    constexpr int kU = kPubWords / 4 / kMainThreads / 2;  // two batches
+    const __amdgpu_buffer_rsrc_t r = dev_rsrc(gpub, 4u * (uint32_t)nent);
+    if (t < nb) {
+      hdr_b = load_dev4(r, 4u * (t * P + 1));
+      hdr_f = load_dev4(r, 4u * (t * P + 2));
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint4 u[kU];
+#pragma unroll
+      for (int j = 0; j < kU; ++j) {
+        const int i = t + (h * kU + j) * kMainThreads;
+        if (i < n4) u[j] = load_dev16(r, 16u * i);
+      }
+#pragma unroll
+      for (int j = 0; j < kU; ++j) {
+        const int i = t + (h * kU + j) * kMainThreads;
+        if (i < n4) reinterpret_cast<uint4*>(cs.pub)[i] = u[j];
+      }
+    }
+  }
+  __syncthreads();
+  dbg_stamp(dbk, 10);
+  // f(word, index) over the union, four uint4 LDS reads in flight per step
+  const auto for_union = [&](auto&& f) {
+    const uint4* p4 = reinterpret_cast<const uint4*>(cs.pub);
+    for (int i0 = t; i0 < n4; i0 += 4 * kMainThreads) {
+      uint4 v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int i = i0 + q * kMainThreads;
+        v[q] = (i < n4) ? p4[i] : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t e = 4u * (uint32_t)(i0 + q * kMainThreads);
+        f(v[q].x, e);
+        f(v[q].y, e + 1u);
+        f(v[q].z, e + 2u);
+        f(v[q].w, e + 3u);
+      }
+    }
+  };
+
+  uint32_t tstar = 0, need3 = 0;
+  if (!all) {
+    // t* must be >= L = (largest list bound) << 20 for the lists to hold
+    // every key >= t*; keys below L never matter.
+    const uint32_t maxB = block_reduce4<2, 0, 0, 0>(make_uint4(hdr_b, 0, 0, 0), cs.wave_tmp).x;
+    const uint32_t L = maxB >= (uint32_t)kNB1 ? 0xffffffffu : max(maxB << 20, kKeyNegInf);
+    dbg_stamp(dbk, 4);
+    uint32_t cL = 0, kmin = 0xffffffffu, kmax = 0;
+    for_union([&](uint32_t w, uint32_t) {
+      const bool in = w >= L;
+      cL += in ? 1u : 0u;
+      kmin = in ? min(kmin, w) : kmin;
+      kmax = in ? max(kmax, w) : kmax;
+    });
+    const uint4 st = block_reduce4<0, 1, 2, 0>(make_uint4(cL, kmin, kmax, 0), cs.wave_tmp);
+    const bool ok = maxB < (uint32_t)kNB1 && st.x >= (uint32_t)K;
+    if (!ok) {
+      dbg_stamp(dbk, 13);
+      coop_select_hist(cs, smem, S, bid, nb, len, p_lo, p_hi, rs, srow, pt_row, o);
+      return;
+    }
+    const uint32_t lo = st.y, hi = st.z;
+    // level 1 over the bit window that spreads [lo, hi] over <= 4096 bins
+    int sh = 0;
+    while (sh < 32 && (hi >> sh) - (lo >> sh) >= (uint32_t)kNB1) ++sh;
+    const uint32_t base = lo >> sh;
+    uint32_t* hist = cs.scan.hist;
+    for (int i = t; i < kNB1; i += kMainThreads) hist[i] = 0u;
+    __syncthreads();
+    for_union([&](uint32_t w, uint32_t) {
+      if (w >= lo) atomicAdd(&hist[(w >> sh) - base], 1u);
+    });
+    __syncthreads();
+    dbg_stamp(dbk, 7);
+    find_threshold_fixed<kNB1, kMainThreads>(hist, (uint32_t)K, cs.wave_tmp, cs.res);
+    uint32_t prefix = cs.res[0] + base;  // == key >> sh
+    dbg_stamp(dbk, 15);
+    if (t == 0 && g_dbg_on && dbk < kDbgBlocks) g_dbg[dbk * kDbgPhases + 12] = (unsigned long long)sh;
+    uint32_t need = (uint32_t)K - cs.res[1];
+    // refine the low sh bits, at most 10 per level
+    while (sh > 0) {
+      const int sub = min(10, sh);
+      sh -= sub;
+      for (int i = t; i < kNB2; i += kMainThreads) hist[i] = 0u;
+      __syncthreads();
+      const int hs = sh + sub;
+      for_union([&](uint32_t w, uint32_t) {
+        if (w >= lo && (w >> hs) == prefix) atomicAdd(&hist[(w >> sh) & ((1u << sub) - 1u)], 1u);
+      });
+      __syncthreads();
+      find_threshold_fixed<kNB2, kMainThreads>(hist, need, cs.wave_tmp, cs.res);
+      prefix = (prefix << sub) | cs.res[0];
+      need -= cs.res[1];
+    }
+    tstar = prefix;
+    need3 = need;
+    dbg_stamp(dbk, 13);
+  }
+  const bool tfin = !all && key_is_finite(tstar);
+
+  // ---- offsets: x = selected above t* before this workgroup, y = ties
+  // before it, z = all selected above t*; all: x = finite before, z = all finite
+  uint4 acc = make_uint4(0, 0, 0, 0);
+  if (all) {
+    acc.x = (t < bid) ? hdr_f : 0u;
+    acc.z = hdr_f;
+  } else {
+    const uint32_t mine0 = (uint32_t)(bid * P);
+    for_union([&](uint32_t w, uint32_t e) {
+      const bool g = w > tstar && key_is_finite(w);  // header words and padding are < tstar
+      const bool before = e < mine0;
+      acc.x += (g && before) ? 1u : 0u;
+      acc.y += (w == tstar && before) ? 1u : 0u;
+      acc.z += g ? 1u : 0u;
+    });
+  }
+  const uint4 r = block_reduce4<0, 0, 0, 0>(acc, cs.wave_tmp);
+  const uint32_t ties_before = r.y;
+  const uint32_t base = r.x + (tfin ? min(ties_before, need3) : 0u);
+  const uint32_t nsel = r.z + (tfin ? need3 : 0u);
+  dbg_stamp(dbk, 14);
+
+  // ---- emit own selections in position order ----
+  uint32_t run_sel = 0, run_tie = ties_before;
+  for (int i0 = 0; i0 < nown; i0 += kMainThreads) {
+    const int i = i0 + t;
+    const bool in = i < nown;
+    const uint32_t k = in ? cs.keys[i] : 0u;
+    const bool tie = in && tfin && k == tstar;
+    uint32_t tie_tot, sel_tot;
+    const uint32_t tie_pre = block_flag_scan(tie, cs.wave_tmp, &tie_tot);
+    const bool sel = in && key_is_finite(k) && (all || k > tstar || (tie && run_tie + tie_pre < need3));
+    const uint32_t sel_pre = block_flag_scan(sel, cs.wave_tmp, &sel_tot);
+    if (sel) {
+      const int p = p_lo + i;
+      o[base + run_sel + sel_pre] = pt_row[p >> 6] * DSA_PAGE_TOKENS + (p & (DSA_PAGE_TOKENS - 1));
+    }
+    run_sel += sel_tot;
+    run_tie += tie_tot;
+  }
+  if (bid == nb - 1)
+    for (int j = (int)nsel + t; j < K; j += kMainThreads) o[j] = -1;
+  dbg_stamp(dbk, 11);
+}
+
 template <int VARIANT>
 __device__ __forceinline__ v4f qk_fp8(const v8i& qa, const v8i& kb) {
   v4f acc = {0.f, 0.f, 0.f, 0.f};
@@ -574,11 +840,30 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   const bool with_hist = S.hist != nullptr;
   const int dbk = blockIdx.x;
   dbg_stamp(dbk, 0);
+  const int cap = min(S.slab_stride, S.pt_stride * DSA_PAGE_TOKENS);
+  const int len = max(0, min(S.seq_lens[row], cap));
+  const int nchunks = (len + kChunkKeys - 1) / kChunkKeys;
+  const int nb = S.blocks_per_row;
+  const int c0 = (int)((long)nchunks * bid / nb);
+  const int c1 = (int)((long)nchunks * (bid + 1) / nb);
+  const int* pt_row = S.page_table + (long)row * S.pt_stride;
+  // this workgroup's page-table entries, prefetched with the query
+  const int pg0 = c0 >> 2;
+  const int npg = (c1 > c0) ? ((c1 - 1) >> 2) - pg0 + 1 : 0;
+  const bool pts_lds = npg <= kScanMaxPages;
   {
+    constexpr int kQ = kHeads * DSA_INDEX_DIM / 16;  // uint4 of the query block
     const uint4* src = reinterpret_cast<const uint4*>(S.q8 + (long)row * kHeads * DSA_INDEX_DIM);
-    for (int i = t; i < kHeads * DSA_INDEX_DIM / 16; i += kMainThreads)
-      reinterpret_cast<uint4*>(sh.qs)[i] = src[i];
-    if (t < kHeads) sh.ws[t] = S.w[(long)row * kHeads + t];
+    uint4 qv = make_uint4(0, 0, 0, 0);
+    if (t < kQ) qv = src[t];
+    const float wv0 = (t < kHeads) ? S.w[(long)row * kHeads + t] : 0.f;
+    const int pv = (pts_lds && t < npg) ? pt_row[pg0 + t] : 0;
+    if (t < kQ) reinterpret_cast<uint4*>(sh.qs)[t] = qv;
+    for (int i = t + kMainThreads; i < kQ; i += kMainThreads) reinterpret_cast<uint4*>(sh.qs)[i] = src[i];
+    if (t < kHeads) sh.ws[t] = wv0;
+    if (pts_lds && t < npg) sh.pts[t] = pv;
+    if (pts_lds)
+      for (int i = t + kMainThreads; i < npg; i += kMainThreads) sh.pts[i] = pt_row[pg0 + i];
     if (with_hist)
       for (int i = t; i < kHistBins; i += kMainThreads) sh.hist[i] = 0u;
     if (S.coop && t < kNumSync) {  // barrier senses: flipped once per use
@@ -586,12 +871,6 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
       reinterpret_cast<CoopShared*>(smem)->sense[t] = group_sense(sync + t * kSyncWords, bid);
     }
   }
-  const int cap = min(S.slab_stride, S.pt_stride * DSA_PAGE_TOKENS);
-  const int len = max(0, min(S.seq_lens[row], cap));
-  const int nchunks = (len + kChunkKeys - 1) / kChunkKeys;
-  const int nb = S.blocks_per_row;
-  const int c0 = (int)((long)nchunks * bid / nb);
-  const int c1 = (int)((long)nchunks * (bid + 1) / nb);
   float* srow = S.scores + (long)row * S.slab_stride;
   {  // slab tail past the last scored chunk -> -inf, spread over the row's blocks
     const long tail0 = (long)nchunks * kChunkKeys;
@@ -624,14 +903,14 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   const int n = c1 - c0;
   const int w0 = c0 + (int)((long)n * wv / kMainWaves);
   const int w1 = c0 + (int)((long)n * (wv + 1) / kMainWaves);
-  const int* pt_row = S.page_table + (long)row * S.pt_stride;
   for (int cb = w0; cb < w1; cb += kScanBatch) {
     uint4 kv[kScanBatch][2];
     float ksc[kScanBatch];
     bool ok[kScanBatch];
     int page[kScanBatch];
 #pragma unroll
-    for (int i = 0; i < kScanBatch; ++i) page[i] = (cb + i < w1) ? pt_row[(cb + i) >> 2] : -1;
+    for (int i = 0; i < kScanBatch; ++i)
+      page[i] = (cb + i < w1) ? (pts_lds ? sh.pts[((cb + i) >> 2) - pg0] : pt_row[(cb + i) >> 2]) : -1;
 #pragma unroll
     for (int i = 0; i < kScanBatch; ++i) {
       const int c = cb + i;
@@ -679,13 +958,16 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
     }
   }
   dbg_stamp(dbk, 2);
+  dbg_stamp_wave(dbk, 5, kMainWaves - 1);
   if (!with_hist) return;
   __syncthreads();
+  dbg_stamp(dbk, 6);
   uint32_t* rs = S.hist + (long)row * S.hist_row_words;
-  for (int i = t; i < kHistBins; i += kMainThreads) {
-    const uint32_t c = sh.hist[i];
-    if (c) atomicAdd(&rs[i], c);
-  }
+  if (!S.coop)
+    for (int i = t; i < kHistBins; i += kMainThreads) {
+      const uint32_t c = sh.hist[i];
+      if (c) atomicAdd(&rs[i], c);
+    }
   dbg_stamp(dbk, 3);
   if (!S.next_idx) return;
   if (S.coop) {

@@ -170,6 +170,35 @@ __device__ __forceinline__ uint32_t block_flag_scan(bool f, uint32_t* wave_tmp, 
   return before + in_wave;
 }
 
+// Block-wide reduction of four per-thread values; OPn: 0 = sum, 1 = min,
+// 2 = max.  wave_tmp: 4 words per wave.
+template <int OP>
+__device__ __forceinline__ uint32_t red_op(uint32_t a, uint32_t b) {
+  return OP == 0 ? a + b : (OP == 1 ? min(a, b) : max(a, b));
+}
+template <int OP0, int OP1, int OP2, int OP3>
+__device__ __forceinline__ uint4 block_reduce4(uint4 v, uint32_t* wave_tmp) {
+  const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave, nw = blockDim.x / kWave;
+  for (int o = 32; o >= 1; o >>= 1) {
+    v.x = red_op<OP0>(v.x, __shfl_xor(v.x, o));
+    v.y = red_op<OP1>(v.y, __shfl_xor(v.y, o));
+    v.z = red_op<OP2>(v.z, __shfl_xor(v.z, o));
+    v.w = red_op<OP3>(v.w, __shfl_xor(v.w, o));
+  }
+  if (lane == 0) *reinterpret_cast<uint4*>(&wave_tmp[4 * wv]) = v;
+  __syncthreads();
+  uint4 r = *reinterpret_cast<const uint4*>(&wave_tmp[0]);
+  for (int i = 1; i < nw; ++i) {
+    const uint4 x = *reinterpret_cast<const uint4*>(&wave_tmp[4 * i]);
+    r.x = red_op<OP0>(r.x, x.x);
+    r.y = red_op<OP1>(r.y, x.y);
+    r.z = red_op<OP2>(r.z, x.z);
+    r.w = red_op<OP3>(r.w, x.w);
+  }
+  __syncthreads();
+  return r;
+}
+
 // Block-wide sums of four per-thread counts.  wave_tmp: 4 words per wave.
 __device__ __forceinline__ uint4 block_sum4(uint4 v, uint32_t* wave_tmp) {
   const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave, nw = blockDim.x / kWave;
@@ -200,6 +229,12 @@ extern __device__ int g_dbg_on;
 extern __device__ unsigned long long g_dbg[kDbgBlocks * kDbgPhases];
 __device__ __forceinline__ void dbg_stamp(int blk, int ph) {
   if (g_dbg_on && threadIdx.x == 0 && blk < kDbgBlocks)
+    g_dbg[blk * kDbgPhases + ph] = __builtin_amdgcn_s_memrealtime();
+}
+
+// Same, recorded by lane 0 of wave `w` instead of thread 0.
+__device__ __forceinline__ void dbg_stamp_wave(int blk, int ph, int w) {
+  if (g_dbg_on && threadIdx.x == (unsigned)(w * kWave) && blk < kDbgBlocks)
     g_dbg[blk * kDbgPhases + ph] = __builtin_amdgcn_s_memrealtime();
 }
 

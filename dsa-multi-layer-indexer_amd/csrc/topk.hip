@@ -62,13 +62,14 @@ constexpr int kSyncGroups = 16;
 constexpr int kSyncFlags = 8;
 constexpr int kSyncLine = 64;  // words
 constexpr int kSyncWords = (kSyncGroups + 1 + kSyncFlags) * kSyncLine;
-constexpr int kNumSync = 2;
+constexpr int kNumSync = 3;
 static_assert(kSyncGroups == kGroupSyncGroups && kSyncFlags == kGroupSyncFlags && kSyncLine == kGroupSyncLine,
               "group-barrier layout");
 __host__ __device__ inline long row_sync_off(int slab) { return kBmOff + bitmap_words(slab) + 2L * kCandCap; }
-__host__ __device__ inline long row_scratch_words(int slab) {
-  return row_sync_off(slab) + (long)kNumSync * kSyncWords;
-}
+// published local top keys of the cooperative select (decode_main.hip)
+constexpr int kPubWords = 16384;
+__host__ __device__ inline long row_pub_off(int slab) { return row_sync_off(slab) + (long)kNumSync * kSyncWords; }
+__host__ __device__ inline long row_scratch_words(int slab) { return row_pub_off(slab) + kPubWords; }
 
 // Exclusive prefix sum over the block (thread order); *total gets the sum.
 // wave_tmp holds one word per wave.
@@ -112,6 +113,34 @@ __device__ __forceinline__ void find_threshold(const uint32_t* hist, int nbins, 
       res[1] = acc;
     }
     acc += h;
+  }
+  __syncthreads();
+}
+
+// find_threshold for a compile-time NBINS / NT (>= 1 bin per thread),
+// every loop unrolled so the LDS reads are in flight together.
+template <int NBINS, int NT>
+__device__ __forceinline__ void find_threshold_fixed(const uint32_t* hist, uint32_t need, uint32_t* wave_tmp,
+                                                     uint32_t* res) {
+  constexpr int kPer = NBINS / NT;
+  static_assert(kPer >= 1 && NBINS % NT == 0, "bins per thread");
+  const int hi = NBINS - (int)threadIdx.x * kPer;
+  uint32_t h[kPer];
+  uint32_t local = 0;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    h[i] = hist[hi - 1 - i];
+    local += h[i];
+  }
+  uint32_t total;
+  uint32_t acc = block_exclusive_scan(local, wave_tmp, &total);
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    if (acc < need && acc + h[i] >= need) {
+      res[0] = (uint32_t)(hi - 1 - i);
+      res[1] = acc;
+    }
+    acc += h[i];
   }
   __syncthreads();
 }
