@@ -3,16 +3,22 @@
 Default workload ("C3"): DeepSeek-V3.2-shape decode
 at 131072-token context, batch 1, one TP-8 share (16 attention heads, the
 full 64x128 indexer), two consecutive layers under the MLI lag schedule --
-layer L attends layer L-1's top-2048 while layer L's indexer runs on a
-second stream -- captured as one hipGraph.  A step is one replay of that
-graph (2 layers).  Inputs are synthetic N(0,1) (fp8 caches, seeded random
-page table of 64-token pages) and resident in HBM before timing starts.
+layer L attends layer L-1's top-2048 while layer L's indexer scan and top-k
+run concurrently -- captured as one hipGraph.  Each layer is ONE launch of
+the fused decode kernel (attention workgroups and indexer-scan/top-k
+workgroups side by side in one grid).  A step is one replay of that graph
+(2 layers).  Inputs are synthetic N(0,1) (fp8 caches, seeded random page
+table of 64-token pages) and resident in HBM before timing starts.
 
 Prints ONE JSON line.  value = microseconds per decode layer (lower is
-better).  Extra fields: tokens/s, indexer-scan GB/s, the MLI hidden
-fraction, the roofline of the dominant kernel (the indexer scan, timed with
-HIP events per launch on its own stream) and the CPU baseline (the
-reference's fp32 decode-row path restated in oracle/, timed on this host).
+better).  Extra fields: tokens/s, the standalone indexer-scan GB/s, the MLI
+hidden fraction, the roofline of the dominant (and only) kernel of the timed
+region -- the fused layer launch, timed with HIP events per replay on the
+stream it is launched on -- and the CPU baseline (the reference's fp32
+decode-row path restated in oracle/, timed on this host).
+
+--profile-main runs only a calibration copy of known size and the timed
+region (for rocprofv3 kernel-trace and counter runs).
 """
 
 from __future__ import annotations
@@ -30,6 +36,9 @@ sys.path.insert(0, str(REPO / "dsa-multi-layer-indexer_amd"))
 sys.path.insert(0, str(REPO))
 
 HBM_PEAK_GBS = 8000.0
+MALL_DEFEAT_BYTES = 768 << 20  # 3x the 256 MB Infinity Cache
+COPY_BYTES = 256 << 20  # calibration copy for the byte counters (read = write = this)
+TRAFFIC_FILE = REPO / "profiles" / "decode_layer_c3_hbm_traffic.md"
 CONFIGS = {
     "c2": dict(lens=[32768], layers=2, indexer_every=1, desc="v32_ctx32768_b1_2layer_mli_graph"),
     "c3": dict(lens=[131072], layers=2, indexer_every=1, desc="v32_ctx131072_b1_2layer_mli_graph"),
@@ -100,6 +109,19 @@ def graph_event_ms(fn, iters: int, torch) -> float:
     return a.elapsed_time(b) / iters
 
 
+def read_traffic():
+    """HBM bytes per fused layer launch measured by the rocprofv3 counter runs
+    (FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy) recorded in
+    profiles/; None when that summary is absent."""
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(ctx: int, budget_s: float = 15.0) -> dict:
     """The reference's fp32 decode-row path (oracle/cpu_reference_path.py) on
     this host's cores, bounded to about budget_s seconds."""
@@ -131,6 +153,10 @@ def main() -> int:
     ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--max-sets", type=int, default=64,
+                    help="cap on the rotated layer sets (1: no Infinity-Cache defeat)")
+    ap.add_argument("--profile-main", action="store_true",
+                    help="only the calibration copy and the timed region (profiler runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only (one TP-8 share of heads); "
@@ -152,35 +178,81 @@ def main() -> int:
     B = len(lens)
     n_layers = cfg["layers"]
     pt, num_pages = S.make_page_table(lens, seed=1000, device=dev)
-    layers = [S.make_decode_layer(lens, seed=1000 * 3 + i, device=dev, page_table=pt,
-                                  num_pages=num_pages, indexer=(i % cfg["indexer_every"] == 0))
-              for i in range(n_layers)]
+    # The scanned index cache and gathered rows of one step (about 37 MB at
+    # C3) would stay in the 256 MB Infinity Cache across replays; a real
+    # model's layers never revisit theirs within a step.  Replays therefore
+    # rotate over enough independent layer sets that each one streams its
+    # inputs from HBM (every set is touched once per `n_sets` replays).
+    step_bytes = n_layers * (scan_bytes(lens) + attn_bytes(B))
+    n_sets = max(1, min(args.max_sets, -(-MALL_DEFEAT_BYTES // step_bytes)))
+    sets = []
+    for k in range(n_sets):
+        layers = [S.make_decode_layer(lens, seed=1000 * 3 + 100 * k + i, device=dev, page_table=pt,
+                                      num_pages=num_pages, indexer=(i % cfg["indexer_every"] == 0))
+                  for i in range(n_layers)]
+        sets.append(layers)
+    layers = sets[0]
     first = S.random_selection(lens, 2048, pt, seed=7, device=dev)
     torch.cuda.synchronize()
 
-    full = MLISchedule(layers, first)
-    attn_only = MLISchedule(layers, first, indexer=False, attend_all_first=True)
-    idx_only = MLISchedule(layers, first, attention=False)
-    for s in (full, attn_only, idx_only):
+    fulls = [MLISchedule(ls, first) for ls in sets]
+    full = fulls[0]
+    attn_onlys = [MLISchedule(ls, first, indexer=False, attend_all_first=True) for ls in sets]
+    idx_onlys = [MLISchedule(ls, first, attention=False) for ls in sets]
+    scheds = fulls + attn_onlys + idx_onlys
+    for s in scheds:
         s.capture()
 
-    for _ in range(args.warmup):
-        full.replay()
-    # ---- timed region: exactly `steps` graph replays ----
+    def rotated(group):
+        state = {"i": 0}
+
+        def fn():
+            group[state["i"] % len(group)].replay()
+            state["i"] += 1
+        return fn
+
+    if args.profile_main:
+        # calibration for the HBM byte counters: a plain copy of known size
+        src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    for i in range(args.warmup):
+        fulls[i % n_sets].replay()
+    # ---- timed region: exactly `steps` graph replays, bracketed by one HIP
+    # event pair on the stream the graphs are launched on ----
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        full.replay()
+    ev0.record()
+    for i in range(args.steps):
+        fulls[i % n_sets].replay()
+    ev1.record()
     torch.cuda.synchronize()
     ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    # every replay is n_layers launches of the one kernel; the figure includes
+    # the launch-to-launch gaps, so it bounds the kernel's duration from above
+    launch_ms = ev0.elapsed_time(ev1) / (args.steps * n_layers)
+    lb = scan_bytes(lens) + attn_bytes(B)
+    if args.profile_main:
+        for s in scheds:
+            s.close()
+        print(json.dumps({"profile_main": True, "sets": n_sets, "us_per_layer": round(ms_step * 1e3 / n_layers, 3),
+                          "launch_us": round(launch_ms * 1e3, 3), "layer_bytes": lb,
+                          "copy_bytes": COPY_BYTES}), flush=True)
+        return 0
 
     reps = max(20, args.steps // 2)
-    t_attn = time_graph(attn_only.replay, reps, torch)
-    t_idx = time_graph(idx_only.replay, reps, torch)
-    t_full = time_graph(full.replay, reps, torch)
+    t_attn = time_graph(rotated(attn_onlys), reps, torch)
+    t_idx = time_graph(rotated(idx_onlys), reps, torch)
+    t_full = time_graph(rotated(fulls), reps, torch)
     hidden = 1.0 - (t_full - t_attn) / t_idx if t_idx > 0 else None
-    # the same schedule without a graph: two streams, and one stream
-    t_eager = time_graph(full.run_eager, reps, torch)
+    # the same schedule without a graph, and layer by layer (one set, cache-warm)
+    t_eager = time_graph(lambda: fulls[0].run_eager(), reps, torch)
 
     def serial():
         att = first
@@ -190,25 +262,37 @@ def main() -> int:
                 att = L.next_idx
     t_serial = time_graph(serial, reps, torch)
 
-    # ---- dominant kernel: indexer scan, per-launch HIP events ----
-    L0 = layers[0]
-    scan = lambda: ops.indexer_scan(L0.q_fp8, L0.w, L0.index_k, L0.page_table, L0.seq_lens,
-                                    L0.slab_stride, out=L0.scores)
+    # ---- the standalone ops (scan-only launches, the two-launch top-k, the
+    # attention alone), each rotating over the sets' first layers ----
+    L0s = [ls[0] for ls in sets]
+
+    def rot_layers(make):
+        fns = [make(L) for L in L0s]
+        state = {"i": 0}
+
+        def fn():
+            fns[state["i"] % len(fns)]()
+            state["i"] += 1
+        return fn
+    scan = rot_layers(lambda L: lambda: ops.indexer_scan(L.q_fp8, L.w, L.index_k, L.page_table,
+                                                         L.seq_lens, L.slab_stride, out=L.scores))
     for _ in range(10):
         scan()
-    scan_ms = graph_event_ms(scan, 100, torch)
+    n_graph = max(50, 2 * n_sets)
+    scan_ms = graph_event_ms(scan, n_graph, torch)
     scan_ms_pairs = event_ms(scan, 100, torch)
     sb = scan_bytes(lens)
     scan_gbs = sb / (scan_ms * 1e-3) / 1e9
-    topk_fn = lambda: ops.topk(L0.scores, L0.seq_lens, 2048, page_table=L0.page_table,
-                               out=L0.next_idx, scratch=L0.topk_scratch)
-    topk_ms = graph_event_ms(topk_fn, 50, torch)
-    attn_fn = lambda: ops.sparse_mla_decode(L0.q_bf16, L0.kv_pool, first, workspace=L0.workspace,
-                                            out=L0.out)
-    attn_ms = graph_event_ms(attn_fn, 50, torch)
+    topk_fn = rot_layers(lambda L: lambda: ops.topk(L.scores, L.seq_lens, 2048, page_table=L.page_table,
+                                                    out=L.next_idx, scratch=L.topk_scratch))
+    topk_ms = graph_event_ms(topk_fn, n_graph, torch)
+    attn_fn = rot_layers(lambda L: lambda: ops.sparse_mla_decode(L.q_bf16, L.kv_pool, first,
+                                                                 workspace=L.workspace, out=L.out))
+    attn_ms = graph_event_ms(attn_fn, n_graph, torch)
     ab = attn_bytes(B)
 
     us_layer = ms_step * 1e3 / n_layers
+    layer_gbs = lb / (launch_ms * 1e-3) / 1e9
     res = {
         "metric": ("\u00b5s per DSA decode layer at 128K ctx (b=1, 16 heads); indexer-scan HBM GB/s"
                    if args.config == "c3" else f"\u00b5s per DSA decode layer ({args.config})"),
@@ -226,25 +310,28 @@ def main() -> int:
         "config": {"workload": cfg["desc"], "batch": B, "ctx": lens if B <= 4 else
                    {"min": min(lens), "max": max(lens), "sum": sum(lens)},
                    "layers_per_step": n_layers, "index_heads": 64, "attn_heads": 16,
-                   "topk": 2048, "page_tokens": 64, "schedule": "MLI lag, 2 streams, 1 hipGraph"},
+                   "topk": 2048, "page_tokens": 64,
+                   "schedule": "MLI lag, one fused launch per layer, 1 hipGraph",
+                   "rotated_sets": n_sets, "bytes_per_step": step_bytes},
         "tokens_per_s": round(B / (us_layer * 1e-6), 1),
         "indexer_scan_GBps": round(scan_gbs, 1),
+        "layer_launch_us": round(launch_ms * 1e3, 3),
         "kernel_us": {"indexer_scan": round(scan_ms * 1e3, 3), "topk": round(topk_ms * 1e3, 3),
                       "sparse_mla+combine": round(attn_ms * 1e3, 3),
                       "indexer_scan_event_pairs": round(scan_ms_pairs * 1e3, 3)},
         "attention_gather_GBps": round(ab / (attn_ms * 1e-3) / 1e9, 1),
-        "mli": {"graph_ms": round(t_full, 5), "eager_2stream_ms": round(t_eager, 5),
+        "mli": {"graph_ms": round(t_full, 5), "eager_ms": round(t_eager, 5),
                 "serial_1stream_ms": round(t_serial, 5), "attn_only_ms": round(t_attn, 5),
                 "indexer_only_ms": round(t_idx, 5),
                 "hidden_fraction": None if hidden is None else round(hidden, 4)},
-        "roofline": {"bound": "hbm", "achieved": round(scan_gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(scan_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "indexer_scan_kernel",
-                     "algorithmic_bytes": sb},
+        "roofline": {"bound": "hbm", "achieved": round(layer_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(layer_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": read_traffic(), "kernel": "decode_main_kernel (fused layer launch)",
+                     "algorithmic_bytes": lb, "launch_us": round(launch_ms * 1e3, 3)},
     }
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(131072 if args.config == "c3" else 8192, args.cpu_budget)
-    for s in (full, attn_only, idx_only):
+    for s in scheds:
         s.close()
     print(json.dumps(res), flush=True)
     return 0

@@ -1,0 +1,49 @@
+"""CPU: the drop-in core ops' argument contract (same ValueErrors as the
+reference's attention_core.py:27-160) and their installation into a module
+that imported the reference names (dsa_layer.py:21-27).  No kernel runs."""
+
+from __future__ import annotations
+
+import types
+
+import pytest
+import torch
+
+
+def _ac():
+    from lagged_indexer_dsa_amd import attention_core as ac
+    return ac
+
+
+def test_shape_errors_match_reference():
+    ac = _ac()
+    with pytest.raises(ValueError):
+        ac.indexer_logits(torch.zeros(1, 2, 3), torch.zeros(1, 4, 128), torch.zeros(1, 2, 3))
+    with pytest.raises(ValueError):
+        ac.indexer_logits(torch.zeros(1, 1, 4, 128), torch.zeros(4, 128), torch.zeros(1, 1, 4))
+    with pytest.raises(ValueError):
+        ac.indexer_logits(torch.zeros(1, 1, 16, 64), torch.zeros(1, 4, 64), torch.zeros(1, 1, 16))
+    with pytest.raises(ValueError):
+        ac.select_topk(torch.zeros(4, 8), 2)
+    with pytest.raises(ValueError):
+        ac.sparse_mla_core(torch.zeros(1, 1, 16, 576), torch.zeros(1, 8, 576), torch.zeros(1, 1, 4), 256)
+    with pytest.raises(ValueError):
+        ac.sparse_mla_core(torch.zeros(1, 1, 8, 576), torch.zeros(1, 8, 576), torch.zeros(1, 1, 4), 512)
+
+
+def test_pad_index_is_skv():
+    assert _ac().pad_index(8192) == 8192
+
+
+def test_install_rebinds_reference_names():
+    ac = _ac()
+    mod = types.SimpleNamespace(indexer_logits=None, select_topk=None, sparse_mla_core=None,
+                                dense_mla_core=None, apply_causal_mask=None, unrelated=1)
+    ac.install(mod)
+    assert mod.indexer_logits is ac.indexer_logits
+    assert mod.select_topk is ac.select_topk
+    assert mod.sparse_mla_core is ac.sparse_mla_core
+    assert mod.dense_mla_core is ac.dense_mla_core
+    assert mod.apply_causal_mask is ac.apply_causal_mask
+    assert mod.unrelated == 1
+    assert not hasattr(mod, "pad_index")
