@@ -3,7 +3,8 @@
  * Attention decode hot path: lightning-indexer scan over a paged fp8 key
  * cache, exact top-k select, split-K sparse MLA over the fp8 656-byte latent
  * pool, and the Multi-layer Indexer (MLI) lag schedule as one captured
- * two-stream hipGraph.
+ * hipGraph of fused per-layer launches (attention and indexer workgroups in
+ * one grid).
  *
  * Conventions (every entry point):
  *   - plain device pointers and sizes; no torch types;
