@@ -66,9 +66,9 @@ struct AttnShared {
   float s[kHG * kTile];                  // scores, log2 domain
   uint16_t p[kHG * kPLd];                // probabilities, bf16
   float m[kHG], l[kHG], alpha[kHG];
-  uint32_t last;
+  uint32_t sense;  // the (row, head group) barrier's flag value at launch
 };
-static_assert(kMaxSplit * 3 * kHG * sizeof(float) <= sizeof(AttnShared::vt), "merge scratch");
+static_assert(kMaxSplit * 3 * kHG * sizeof(float) + kMainThreads * 16 <= sizeof(AttnShared::vt), "merge scratch");
 
 __device__ __forceinline__ v4f mfma_bf16(const uint4& a, const uint4& b, v4f c) {
   v8bf av, bv;
@@ -125,6 +125,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
   const int lane = t & (kWave - 1);
   const int wv = wave_id();
   const int kr = lane & 15, kc = lane >> 4;
+  if (t == 0) sh.sense = group_sense(A.sync + ((long)b * nhg + hg) * kSyncWords, sp);
   const int kps = (A.topk + nsplit - 1) / nsplit;
   const int k0 = min(A.topk, sp * kps), k1 = min(A.topk, k0 + kps);
   const int* idx_row = A.idx + (long)b * A.topk;
@@ -265,44 +266,36 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
     store_dev(&A.part_ml[pblk * (2 * kHG) + 2 * t + 1], sh.l[t]);
   }
 
-  // arrival: the partials went out with device-scope stores; wait for them,
-  // then count -- the last split of (row, head group) merges
-  wait_mem();
-  __syncthreads();
-  if (t == 0) {
-    const uint32_t prev = atomicAdd(&A.counters[(long)b * nhg + hg], 1u);
-    sh.last = (prev == (uint32_t)nsplit - 1u) ? 1u : 0u;
-  }
-  __syncthreads();
+  // every split of (row, head group) waits for the others' partials, then
+  // merges a 1/nsplit slice of the 16 x 512 outputs
+  group_barrier(A.sync + ((long)b * nhg + hg) * kSyncWords, sp, nsplit, sh.sense);
   dbg_stamp(dbk, 4);
-  if (!sh.last) return;
-  if (t == 0) A.counters[(long)b * nhg + hg] = 0u;  // re-arm for the next call
-  dbg_stamp(dbk, 5);
 
   // log-sum-exp merge (reference combine_kernel K:996-1045):
-  // m* = max m_s, L = sum l_s 2^(m_s - m*), out = sum O_s 2^(m_s - m*) / L.
-  // 16 heads x 512 dims = 2048 float4 outputs, 4 per thread: two rounds of
-  // 2 outputs x 16 splits of device-scope loads, the first round issued
-  // together with the (m, l) loads.
+  // m* = max m_s, L = sum l_s 2^(m_s - m*), out = sum O_s 2^(m_s - m*) / L,
+  // the splits summed in a fixed order (deterministic output).
+  constexpr int kVec = kHG * DSA_LATENT_DIM / 4;  // float4 outputs of the group
   float* mls = reinterpret_cast<float*>(sh.vt);
   float* wgt = mls + kMaxSplit * 2 * kHG;
+  float4* red = reinterpret_cast<float4*>(wgt + kMaxSplit * kHG);
   const float* pbase = A.part_o + pblk0 * (kHG * DSA_LATENT_DIM);
   const __amdgpu_buffer_rsrc_t prs = dev_rsrc(pbase, (uint32_t)nsplit * kHG * DSA_LATENT_DIM * 4u);
   const __amdgpu_buffer_rsrc_t mrs = dev_rsrc(A.part_ml + pblk0 * 2 * kHG, nsplit * 2 * kHG * 4u);
-  constexpr int kMS = 16;              // splits per load round
-  constexpr int kOut = 2;              // float4 outputs per round
-  constexpr int kVec = kHG * DSA_LATENT_DIM / 4;
-  auto load_round = [&](float4 (&x)[kOut][kMS], int v0, int s0) {
+  const int v_lo = (int)((long)kVec * sp / nsplit), nv = (int)((long)kVec * (sp + 1) / nsplit) - v_lo;
+  const int span = min(nv, kMainThreads);  // outputs per round
+  int G = 1;                               // thread groups over the splits
+  while (2 * G * span <= kMainThreads && 2 * G <= nsplit) G *= 2;
+  const int spg = (nsplit + G - 1) / G;
+  const int g = t / span;
+  constexpr int kLd = 8;                   // partial loads in flight per thread
+  float4 x[kLd];
+  auto load_x = [&](int v, int s0, int s1) {
 #pragma unroll
-    for (int o2 = 0; o2 < kOut; ++o2)
-#pragma unroll
-      for (int i = 0; i < kMS; ++i)
-        x[o2][i] = (s0 + i < nsplit)
-                       ? __builtin_bit_cast(float4, load_dev16(prs, 16u * ((s0 + i) * kVec + v0 + o2 * kMainThreads)))
-                       : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i = 0; i < kLd; ++i)
+      x[i] = (s0 + i < s1) ? __builtin_bit_cast(float4, load_dev16(prs, 16u * ((s0 + i) * kVec + v)))
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
   };
-  float4 x[kOut][kMS];
-  load_round(x, t, 0);
+  if (g < G && t - g * span < nv) load_x(v_lo + t - g * span, g * spg, min(nsplit, (g + 1) * spg));
   {  // nsplit*32 floats, <= 8 per thread
     constexpr int kPer = kMaxSplit * 2 * kHG / kMainThreads;
     float v[kPer];
@@ -319,45 +312,55 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
   if (t < kHG) {
     const float* ml = mls + 2 * t;
     float mx = -INFINITY;
-    for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, ml[s * 2 * kHG]);
+    for (int s2 = 0; s2 < nsplit; ++s2) mx = fmaxf(mx, ml[s2 * 2 * kHG]);
     float L = 0.f;
     if (mx != -INFINITY)
-      for (int s = 0; s < nsplit; ++s) {
-        const float ms = ml[s * 2 * kHG];
-        if (ms != -INFINITY) L += ml[s * 2 * kHG + 1] * exp2f(ms - mx);
+      for (int s2 = 0; s2 < nsplit; ++s2) {
+        const float ms = ml[s2 * 2 * kHG];
+        if (ms != -INFINITY) L += ml[s2 * 2 * kHG + 1] * exp2f(ms - mx);
       }
     const float inv = (mx != -INFINITY && L > 0.f) ? 1.f / L : 0.f;
-    for (int s = 0; s < nsplit; ++s) {
-      const float ms = ml[s * 2 * kHG];
-      wgt[s * kHG + t] = (ms != -INFINITY) ? exp2f(ms - mx) * inv : 0.f;
+    for (int s2 = 0; s2 < nsplit; ++s2) {
+      const float ms = ml[s2 * 2 * kHG];
+      wgt[s2 * kHG + t] = (ms != -INFINITY) ? exp2f(ms - mx) * inv : 0.f;
     }
   }
   __syncthreads();
-  dbg_stamp(dbk, 6);
-  for (int v0 = t; v0 < kVec; v0 += kOut * kMainThreads) {
-    float4 acc[kOut];
+  dbg_stamp(dbk, 5);
+  for (int r0 = 0; r0 < nv; r0 += span) {
+    const int vi = r0 + t - g * span;
+    const bool active = g < G && vi < nv;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (active) {
+      const int v = v_lo + vi;
+      const int h = v / (DSA_LATENT_DIM / 4);
+      const int s0 = g * spg, s1 = min(nsplit, s0 + spg);
+      for (int sb = s0; sb < s1; sb += kLd) {
+        if (r0 != 0 || sb != s0) load_x(v, sb, s1);
 #pragma unroll
-    for (int o2 = 0; o2 < kOut; ++o2) acc[o2] = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s0 = 0; s0 < nsplit; s0 += kMS) {
-      if (v0 != t || s0 != 0) load_round(x, v0, s0);
-#pragma unroll
-      for (int o2 = 0; o2 < kOut; ++o2) {
-        const int h = (v0 + o2 * kMainThreads) / (DSA_LATENT_DIM / 4);
-#pragma unroll
-        for (int i = 0; i < kMS; ++i) {
-          const float wt = (s0 + i < nsplit) ? wgt[(s0 + i) * kHG + h] : 0.f;
-          acc[o2].x += x[o2][i].x * wt; acc[o2].y += x[o2][i].y * wt;
-          acc[o2].z += x[o2][i].z * wt; acc[o2].w += x[o2][i].w * wt;
+        for (int i = 0; i < kLd; ++i) {
+          const float wt = (sb + i < s1) ? wgt[(sb + i) * kHG + h] : 0.f;
+          acc.x += x[i].x * wt; acc.y += x[i].y * wt;
+          acc.z += x[i].z * wt; acc.w += x[i].w * wt;
         }
       }
     }
-#pragma unroll
-    for (int o2 = 0; o2 < kOut; ++o2) {
-      const int v = v0 + o2 * kMainThreads;
+    if (G > 1) {
+      if (active) red[t] = acc;
+      __syncthreads();
+      if (g == 0 && active)
+        for (int k = 1; k < G; ++k) {
+          const float4 y = red[k * span + t];
+          acc.x += y.x; acc.y += y.y; acc.z += y.z; acc.w += y.w;
+        }
+      __syncthreads();
+    }
+    if (g == 0 && active) {
+      const int v = v_lo + vi;
       const int h = v / (DSA_LATENT_DIM / 4);
       uint2 pk;
-      pk.x = pack_bf16x2(acc[o2].x, acc[o2].y);
-      pk.y = pack_bf16x2(acc[o2].z, acc[o2].w);
+      pk.x = pack_bf16x2(acc.x, acc.y);
+      pk.y = pack_bf16x2(acc.z, acc.w);
       const int d = (v % (DSA_LATENT_DIM / 4)) * 4;
       *reinterpret_cast<uint2*>(A.out + ((long)b * A.H + hg * kHG + h) * DSA_LATENT_DIM + d) = pk;
     }
@@ -376,7 +379,7 @@ constexpr int kScanMaxPages = 4100;  // page-table entries a workgroup prefetche
 struct ScanShared {
   uint8_t qs[64 * DSA_INDEX_DIM];
   float ws[64];
-  uint32_t hist[kHistBins];
+  uint32_t hist[kHistBins + 64];  // + spill bins for branch-free updates
   int pts[kScanMaxPages];
 };
 
@@ -384,7 +387,8 @@ struct ScanShared {
 // positions and takes part in the row's selection.
 constexpr int kCoopKeys = 8192;      // positions per workgroup
 constexpr int kCoopMaxBlocks = 256;  // workgroups per row
-constexpr int kPubHdr = 4;           // published list: count, bound, finite count, -
+constexpr int kPubHdr = 4;           // list header: count, bound bin, finite count, max key
+constexpr int kCoopCand = 1024;      // threshold-bin candidates resolved by rank counting
 struct CoopShared {
   ScanShared scan;
   uint32_t keys[kCoopKeys];
@@ -397,17 +401,19 @@ struct CoopShared {
   };
   uint32_t gts[kCoopMaxBlocks];
   uint32_t wave_tmp[4 * kMainWaves];
-  uint32_t res[2];
+  uint32_t res[4];
   uint32_t misc[4];
   uint32_t sense[kNumSync];
+  uint32_t ck[kCoopCand];  // threshold-bin candidates: key, union entry index
+  uint32_t ce[kCoopCand];
 };
 
-// Words per workgroup in the published-key area (a multiple of 4): about
-// three times a workgroup's expected share of the K selected keys plus 16,
-// within the area.  A list too short for its workgroup only costs the
-// fallback to the histogram form.
+// Keys per workgroup list (a multiple of 4): about three times a
+// workgroup's expected share of the K selected keys plus 16, within the
+// area.  A list too short for its workgroup only costs the fallback to the
+// histogram form.
 __host__ __device__ inline int pub_stride(int nb, int K) {
-  const int want = kPubHdr + 3 * ((K + nb - 1) / nb) + 16;
+  const int want = 3 * ((K + nb - 1) / nb) + 16;
   return min((want + 3) & ~3, (kPubWords / nb) & ~3);
 }
 
@@ -574,8 +580,9 @@ __device__ __forceinline__ void coop_select_hist(CoopShared& cs, unsigned char* 
     const bool in = i < nown;
     const uint32_t k = in ? cs.keys[i] : 0u;
     const bool tie = in && tfin && k == tstar;
-    uint32_t tie_tot, sel_tot;
-    const uint32_t tie_pre = block_flag_scan(tie, cs.wave_tmp, &tie_tot);
+    uint32_t tie_tot = 0, sel_tot;
+    uint32_t tie_pre = 0;
+    if (__syncthreads_or(tie)) tie_pre = block_flag_scan(tie, cs.wave_tmp, &tie_tot);
     bool sel;
     if (all) {
       sel = in && key_is_finite(k);
@@ -622,8 +629,9 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
   const bool all = len <= K;
   const int nown = max(0, p_hi - p_lo);
   const int P = pub_stride(nb, K);
-  const uint32_t M = (uint32_t)(P - kPubHdr);
-  uint32_t* gpub = rs + row_pub_off(S.slab_stride);
+  const uint32_t M = (uint32_t)P;
+  uint32_t* ghdr = rs + row_pub_off(S.slab_stride);  // [nb][kPubHdr]
+  uint32_t* gpub = ghdr + kPubHdrWords;              // [nb][P] keys, zero-padded
   uint32_t* sync = rs + row_sync_off(S.slab_stride);
   const int dbk = blockIdx.x;
 
@@ -638,23 +646,25 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
   }
   if (t == 0) cs.misc[0] = 0u;
   __syncthreads();
-  uint32_t nfin = 0;
+  uint32_t nfin = 0, kmax_own = 0;
   for (int i = t; i < nown; i += kMainThreads) {
     const uint32_t k = cs.keys[i];
     nfin += key_is_finite(k) ? 1u : 0u;
-    if ((k >> 20) >= Bb) cs.pub[atomicAdd(&cs.misc[0], 1u)] = k;
+    if ((k >> 20) >= Bb) {
+      cs.pub[atomicAdd(&cs.misc[0], 1u)] = k;
+      kmax_own = max(kmax_own, k);
+    }
   }
-  const uint32_t fin_own = block_reduce4<0, 0, 0, 0>(make_uint4(nfin, 0, 0, 0), cs.wave_tmp).x;
+  const uint4 own = block_reduce4<0, 2, 0, 0>(make_uint4(nfin, kmax_own, 0, 0), cs.wave_tmp);
+  const uint32_t fin_own = own.x;
   {
     const uint32_t cnt = cs.misc[0];
     uint32_t* mine = gpub + (long)bid * P;
-    for (int i = t; i < P; i += kMainThreads) {
-      uint32_t v = 0u;
-      if (i == 0) v = cnt;
-      else if (i == 1) v = Bb;
-      else if (i == 2) v = fin_own;
-      else if (i >= kPubHdr && (uint32_t)(i - kPubHdr) < cnt) v = cs.pub[i - kPubHdr];
-      store_dev(&mine[i], v);
+    if (!all)
+      for (int i = t; i < P; i += kMainThreads) store_dev(&mine[i], (uint32_t)i < cnt ? cs.pub[i] : 0u);
+    if (t < kPubHdr) {
+      const uint32_t v = t == 0 ? cnt : (t == 1 ? Bb : (t == 2 ? fin_own : own.y));
+      store_dev(&ghdr[bid * kPubHdr + t], v);
     }
   }
   dbg_stamp(dbk, 8);
@@ -662,16 +672,18 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
   dbg_stamp(dbk, 9);
 
   // ---- every workgroup: all lists into LDS (one batch of device-scope
-  // loads), the headers' bounds and finite counts ----
-  const int nent = nb * P;
+  // loads), each list's bound bin, finite count and max key ----
+  const int nent = all ? 0 : nb * P;
   const int n4 = nent >> 2;
-  uint32_t hdr_b = 0, hdr_f = 0;
+  uint32_t hdr_b = 0, hdr_f = 0, hdr_m = 0;
   {
     constexpr int kU = kPubWords / 4 / kMainThreads / 2;  // two batches
     const __amdgpu_buffer_rsrc_t r = dev_rsrc(gpub, 4u * (uint32_t)nent);
     if (t < nb) {
-      hdr_b = load_dev4(r, 4u * (t * P + 1));
-      hdr_f = load_dev4(r, 4u * (t * P + 2));
+      const uint4 h = load_dev16(dev_rsrc(ghdr, 16u * (uint32_t)nb), 16u * t);
+      hdr_b = h.y;
+      hdr_f = h.z;
+      hdr_m = h.w;
     }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -681,6 +693,8 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
         const int i = t + (h * kU + j) * kMainThreads;
         if (i < n4) u[j] = load_dev16(r, 16u * i);
       }
+      if (h == 0)
+        for (int i = t; i < kNB1; i += kMainThreads) cs.scan.hist[i] = 0u;
 #pragma unroll
       for (int j = 0; j < kU; ++j) {
         const int i = t + (h * kU + j) * kMainThreads;
@@ -688,6 +702,7 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
       }
     }
   }
+  if (t == 0) cs.misc[1] = 0u;
   __syncthreads();
   dbg_stamp(dbk, 10);
   // f(word, index) over the union, four uint4 LDS reads in flight per step
@@ -712,81 +727,130 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
   };
 
   uint32_t tstar = 0, need3 = 0;
-  if (!all) {
+  // x = selected above t* before this workgroup, y = ties before it,
+  // z = all selected above t*; all: x = finite before, z = all finite
+  uint4 acc = make_uint4(0, 0, 0, 0);
+  const uint32_t mine0 = (uint32_t)(bid * P);
+  if (all) {
+    acc.x = (t < bid) ? hdr_f : 0u;
+    acc.z = hdr_f;
+  } else {
     // t* must be >= L = (largest list bound) << 20 for the lists to hold
     // every key >= t*; keys below L never matter.
-    const uint32_t maxB = block_reduce4<2, 0, 0, 0>(make_uint4(hdr_b, 0, 0, 0), cs.wave_tmp).x;
-    const uint32_t L = maxB >= (uint32_t)kNB1 ? 0xffffffffu : max(maxB << 20, kKeyNegInf);
+    const uint4 hr = block_reduce4<2, 2, 0, 0>(make_uint4(hdr_b, hdr_m, 0, 0), cs.wave_tmp);
+    const uint32_t maxB = hr.x, hi = hr.y;
+    const uint32_t lo = max(maxB << 20, kKeyNegInf);
+    bool ok = maxB < (uint32_t)kNB1 && hi >= lo;
+    uint32_t T1 = 0, above = 0;
+    int sh = 0;
+    if (ok) {
+      // level 1 over the bit window that spreads [lo, hi] over <= 4096 bins
+      while (sh < 32 && (hi >> sh) - (lo >> sh) >= (uint32_t)kNB1) ++sh;
+      const uint32_t base = lo >> sh;
+      uint32_t* hist = cs.scan.hist;
+      // branch-free: keys below lo land in 32 spill bins past the histogram
+      const uint32_t spill = kNB1 + (t & 31);
+      for_union([&](uint32_t w, uint32_t) {
+        atomicAdd(&hist[w >= lo ? (w >> sh) - base : spill], 1u);
+      });
+      __syncthreads();
+      find_threshold_fixed<kNB1, kMainThreads>(hist, (uint32_t)K, cs.wave_tmp, cs.res);
+      ok = cs.res[2] >= (uint32_t)K;  // the union holds at least K keys >= lo
+      T1 = cs.res[0] + base;          // == t* >> sh
+      above = cs.res[1];
+    }
     dbg_stamp(dbk, 4);
-    uint32_t cL = 0, kmin = 0xffffffffu, kmax = 0;
-    for_union([&](uint32_t w, uint32_t) {
-      const bool in = w >= L;
-      cL += in ? 1u : 0u;
-      kmin = in ? min(kmin, w) : kmin;
-      kmax = in ? max(kmax, w) : kmax;
-    });
-    const uint4 st = block_reduce4<0, 1, 2, 0>(make_uint4(cL, kmin, kmax, 0), cs.wave_tmp);
-    const bool ok = maxB < (uint32_t)kNB1 && st.x >= (uint32_t)K;
     if (!ok) {
       dbg_stamp(dbk, 13);
       coop_select_hist(cs, smem, S, bid, nb, len, p_lo, p_hi, rs, srow, pt_row, o);
       return;
     }
-    const uint32_t lo = st.y, hi = st.z;
-    // level 1 over the bit window that spreads [lo, hi] over <= 4096 bins
-    int sh = 0;
-    while (sh < 32 && (hi >> sh) - (lo >> sh) >= (uint32_t)kNB1) ++sh;
-    const uint32_t base = lo >> sh;
-    uint32_t* hist = cs.scan.hist;
-    for (int i = t; i < kNB1; i += kMainThreads) hist[i] = 0u;
-    __syncthreads();
-    for_union([&](uint32_t w, uint32_t) {
-      if (w >= lo) atomicAdd(&hist[(w >> sh) - base], 1u);
+    // pass 2: keys above T1's bin count directly; T1's bin -> candidates
+    for_union([&](uint32_t w, uint32_t e) {
+      const uint32_t bin = w >> sh;
+      const bool in = w >= lo;  // also excludes padding
+      const uint32_t g = (in && bin > T1 && key_is_finite(w)) ? 1u : 0u;
+      acc.x += (e < mine0) ? g : 0u;
+      acc.z += g;
+      if (in && bin == T1) {
+        const uint32_t slot = atomicAdd(&cs.misc[1], 1u);
+        if (slot < (uint32_t)kCoopCand) {
+          cs.ck[slot] = w;
+          cs.ce[slot] = e;
+        }
+      }
     });
     __syncthreads();
     dbg_stamp(dbk, 7);
-    find_threshold_fixed<kNB1, kMainThreads>(hist, (uint32_t)K, cs.wave_tmp, cs.res);
-    uint32_t prefix = cs.res[0] + base;  // == key >> sh
-    dbg_stamp(dbk, 15);
-    if (t == 0 && g_dbg_on && dbk < kDbgBlocks) g_dbg[dbk * kDbgPhases + 12] = (unsigned long long)sh;
-    uint32_t need = (uint32_t)K - cs.res[1];
-    // refine the low sh bits, at most 10 per level
-    while (sh > 0) {
-      const int sub = min(10, sh);
-      sh -= sub;
-      for (int i = t; i < kNB2; i += kMainThreads) hist[i] = 0u;
+    const int sh0 = sh;
+    const uint32_t nc = cs.misc[1];
+    const uint32_t need = (uint32_t)K - above;  // 1 <= need <= nc
+    if (nc <= (uint32_t)kCoopCand) {
+      // exact t* by rank counting: the candidate c with
+      // #{> c} < need <= #{>= c}
+      for (uint32_t j = t; j < nc; j += kMainThreads) {
+        const uint32_t c = cs.ck[j];
+        uint32_t gtc = 0, gec = 0;
+        for (uint32_t i = 0; i < nc; ++i) {
+          const uint32_t x = cs.ck[i];
+          gtc += (x > c) ? 1u : 0u;
+          gec += (x >= c) ? 1u : 0u;
+        }
+        if (gtc < need && need <= gec) {
+          cs.res[0] = c;
+          cs.res[1] = need - gtc;
+        }
+      }
       __syncthreads();
-      const int hs = sh + sub;
-      for_union([&](uint32_t w, uint32_t) {
-        if (w >= lo && (w >> hs) == prefix) atomicAdd(&hist[(w >> sh) & ((1u << sub) - 1u)], 1u);
-      });
-      __syncthreads();
-      find_threshold_fixed<kNB2, kMainThreads>(hist, need, cs.wave_tmp, cs.res);
-      prefix = (prefix << sub) | cs.res[0];
-      need -= cs.res[1];
+      tstar = cs.res[0];
+      need3 = cs.res[1];
+    } else {
+      // many keys share T1's bin: refine its low sh bits, <= 10 per level
+      uint32_t* hist = cs.scan.hist;
+      uint32_t prefix = T1, nd = need;
+      while (sh > 0) {
+        const int sub = min(10, sh);
+        sh -= sub;
+        for (int i = t; i < kNB2; i += kMainThreads) hist[i] = 0u;
+        __syncthreads();
+        const int hs = sh + sub;
+        for_union([&](uint32_t w, uint32_t) {
+          if (w >= lo && (w >> hs) == prefix) atomicAdd(&hist[(w >> sh) & ((1u << sub) - 1u)], 1u);
+        });
+        __syncthreads();
+        find_threshold_fixed<kNB2, kMainThreads>(hist, nd, cs.wave_tmp, cs.res);
+        prefix = (prefix << sub) | cs.res[0];
+        nd -= cs.res[1];
+      }
+      tstar = prefix;
+      need3 = nd;
     }
-    tstar = prefix;
-    need3 = need;
+    dbg_stamp(dbk, 15);
+    // the candidates' share of the offsets
+    if (nc <= (uint32_t)kCoopCand) {
+      for (uint32_t j = t; j < nc; j += kMainThreads) {
+        const uint32_t w = cs.ck[j];
+        const bool g = w > tstar && key_is_finite(w);
+        const bool before = cs.ce[j] < mine0;
+        acc.x += (g && before) ? 1u : 0u;
+        acc.y += (w == tstar && before) ? 1u : 0u;
+        acc.z += g ? 1u : 0u;
+      }
+    } else {
+      // the bin-T1 keys' share, from the union (keys above the bin were
+      // counted in pass 2)
+      for_union([&](uint32_t w, uint32_t e) {
+        if (w < lo || (w >> sh0) != T1) return;
+        const bool g = w > tstar && key_is_finite(w);
+        const bool before = e < mine0;
+        acc.x += (g && before) ? 1u : 0u;
+        acc.y += (w == tstar && before) ? 1u : 0u;
+        acc.z += g ? 1u : 0u;
+      });
+    }
     dbg_stamp(dbk, 13);
   }
   const bool tfin = !all && key_is_finite(tstar);
-
-  // ---- offsets: x = selected above t* before this workgroup, y = ties
-  // before it, z = all selected above t*; all: x = finite before, z = all finite
-  uint4 acc = make_uint4(0, 0, 0, 0);
-  if (all) {
-    acc.x = (t < bid) ? hdr_f : 0u;
-    acc.z = hdr_f;
-  } else {
-    const uint32_t mine0 = (uint32_t)(bid * P);
-    for_union([&](uint32_t w, uint32_t e) {
-      const bool g = w > tstar && key_is_finite(w);  // header words and padding are < tstar
-      const bool before = e < mine0;
-      acc.x += (g && before) ? 1u : 0u;
-      acc.y += (w == tstar && before) ? 1u : 0u;
-      acc.z += g ? 1u : 0u;
-    });
-  }
   const uint4 r = block_reduce4<0, 0, 0, 0>(acc, cs.wave_tmp);
   const uint32_t ties_before = r.y;
   const uint32_t base = r.x + (tfin ? min(ties_before, need3) : 0u);
@@ -800,8 +864,9 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
     const bool in = i < nown;
     const uint32_t k = in ? cs.keys[i] : 0u;
     const bool tie = in && tfin && k == tstar;
-    uint32_t tie_tot, sel_tot;
-    const uint32_t tie_pre = block_flag_scan(tie, cs.wave_tmp, &tie_tot);
+    uint32_t tie_tot = 0, sel_tot;
+    uint32_t tie_pre = 0;
+    if (__syncthreads_or(tie)) tie_pre = block_flag_scan(tie, cs.wave_tmp, &tie_tot);
     const bool sel = in && key_is_finite(k) && (all || k > tstar || (tie && run_tie + tie_pre < need3));
     const uint32_t sel_pre = block_flag_scan(sel, cs.wave_tmp, &sel_tot);
     if (sel) {
@@ -1040,17 +1105,23 @@ static int device_cus() {
 
 int attn_auto_nsplit(int topk) { return std::max(1, std::min(kMaxSplit, (topk + kTile - 1) / kTile)); }
 
+// [partials o | partials (m, l) | pad to 64 words | one group barrier per
+// (row, head group)]
+static size_t attn_partial_words(size_t blocks) {
+  return (blocks * kHG * (DSA_LATENT_DIM + 2) + 63) / 64 * 64;
+}
+
 size_t attn_workspace_bytes(int B, int H, int nsplit) {
   const size_t blocks = (size_t)B * (H / kHG) * nsplit;
-  const size_t counters = ((size_t)B * (H / kHG) + 63) / 64 * 64;
-  return (blocks * kHG * (DSA_LATENT_DIM + 2) + counters) * sizeof(float);
+  const size_t sync = (size_t)B * (H / kHG) * kSyncWords;
+  return (attn_partial_words(blocks) + sync) * sizeof(float);
 }
 
 void attn_bind_workspace(AttnArgs& A, void* ws, int B) {
   const size_t blocks = (size_t)B * (A.H / kHG) * A.nsplit;
   A.part_o = reinterpret_cast<float*>(ws);
   A.part_ml = A.part_o + blocks * kHG * DSA_LATENT_DIM;
-  A.counters = reinterpret_cast<uint32_t*>(A.part_ml + blocks * 2 * kHG);
+  A.sync = reinterpret_cast<uint32_t*>(A.part_o) + attn_partial_words(blocks);
 }
 
 int scan_blocks_per_row(int B, int pt_stride, int slab_stride, int att_blocks, bool big_lds) {

@@ -15,7 +15,7 @@ struct AttnArgs {
   const int* idx;        // [B, topk] KV slots
   float* part_o;         // [B, H/16, nsplit, 16, 512]
   float* part_ml;        // [B, H/16, nsplit, 16, 2]
-  uint32_t* counters;    // [B, H/16] arrival counters, zero between calls
+  uint32_t* sync;        // [B, H/16] group barriers of the splits, zero before first use
   uint16_t* out;         // [B, H, 512] bf16
   int H, topk, nsplit;
   float sm_log2;         // sm_scale * log2(e)

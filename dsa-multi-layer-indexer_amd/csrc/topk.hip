@@ -66,10 +66,14 @@ constexpr int kNumSync = 3;
 static_assert(kSyncGroups == kGroupSyncGroups && kSyncFlags == kGroupSyncFlags && kSyncLine == kGroupSyncLine,
               "group-barrier layout");
 __host__ __device__ inline long row_sync_off(int slab) { return kBmOff + bitmap_words(slab) + 2L * kCandCap; }
-// published local top keys of the cooperative select (decode_main.hip)
+// published local top keys of the cooperative select (decode_main.hip):
+// kPubHdrWords of per-workgroup headers, then kPubWords of key lists
 constexpr int kPubWords = 16384;
+constexpr int kPubHdrWords = 4 * 256;
 __host__ __device__ inline long row_pub_off(int slab) { return row_sync_off(slab) + (long)kNumSync * kSyncWords; }
-__host__ __device__ inline long row_scratch_words(int slab) { return row_pub_off(slab) + kPubWords; }
+__host__ __device__ inline long row_scratch_words(int slab) {
+  return row_pub_off(slab) + kPubHdrWords + kPubWords;
+}
 
 // Exclusive prefix sum over the block (thread order); *total gets the sum.
 // wave_tmp holds one word per wave.
@@ -118,7 +122,8 @@ __device__ __forceinline__ void find_threshold(const uint32_t* hist, int nbins, 
 }
 
 // find_threshold for a compile-time NBINS / NT (>= 1 bin per thread),
-// every loop unrolled so the LDS reads are in flight together.
+// every loop unrolled so the LDS reads are in flight together; also writes
+// the histogram's total to res[2] (res: 3 words).
 template <int NBINS, int NT>
 __device__ __forceinline__ void find_threshold_fixed(const uint32_t* hist, uint32_t need, uint32_t* wave_tmp,
                                                      uint32_t* res) {
@@ -134,6 +139,7 @@ __device__ __forceinline__ void find_threshold_fixed(const uint32_t* hist, uint3
   }
   uint32_t total;
   uint32_t acc = block_exclusive_scan(local, wave_tmp, &total);
+  if (threadIdx.x == 0) res[2] = total;
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     if (acc < need && acc + h[i] >= need) {
@@ -315,7 +321,7 @@ struct FinShared {
   uint32_t hist[kNB1];
   int pt[kMaxWords / 2];  // page-table row (DSA_TOPK_MAX_CTX / 64 pages)
   uint32_t wave_tmp[16];
-  uint32_t res[2];
+  uint32_t res[4];
   uint32_t woff[kSliceThreads / kWave + 1];
   uint32_t ncand;
   uint32_t last;

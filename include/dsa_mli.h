@@ -122,9 +122,10 @@ int dsa_topk(const float* scores, const int32_t* seq_lens,
  *   q         [B, H, 576] bf16;     kv_pool [kv_rows, 656] bytes
  *   idx       [B, topk] int32 KV slots
  *   workspace dsa_sparse_mla_workspace_bytes(B, H, nsplit) bytes: split
- *             partials plus per-(row, head group) arrival counters; zero-fill
- *             it once before the first call, every call leaves the counters
- *             zero again.  Calls that overlap in time must not share it.
+ *             partials plus one barrier per (row, head group) through which
+ *             the splits merge together; zero-fill it once before the first
+ *             call, every call leaves the barriers ready for the next.
+ *             Calls that overlap in time must not share it.
  *   out       [B, H, 512] bf16
  * H must be a multiple of 16; 1 <= nsplit <= 128 (nsplit=0: automatic, and
  * a workspace sized with nsplit=0 fits any nsplit).
