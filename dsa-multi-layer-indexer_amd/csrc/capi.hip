@@ -363,3 +363,7 @@ extern "C" int dsa_internal_set_coop_select(int on) {
   return DSA_OK;
 }
 extern "C" int dsa_internal_group_wait_timeouts(int reset) { return dsa::group_wait_timeouts(reset); }
+extern "C" int dsa_internal_set_scan_blocks_cap(int n) {
+  dsa::set_scan_blocks_cap(n);
+  return DSA_OK;
+}

@@ -1124,13 +1124,17 @@ void attn_bind_workspace(AttnArgs& A, void* ws, int B) {
   A.sync = reinterpret_cast<uint32_t*>(A.part_o) + attn_partial_words(blocks);
 }
 
+static int g_scan_blocks_cap = 0;  // internal: cap on scan workgroups per launch (0 = none)
+void set_scan_blocks_cap(int n) { g_scan_blocks_cap = std::max(0, n); }
+
 int scan_blocks_per_row(int B, int pt_stride, int slab_stride, int att_blocks, bool big_lds) {
   const long cap = std::min((long)slab_stride, (long)pt_stride * DSA_PAGE_TOKENS);
   const long cap_chunks = (cap + kChunkKeys - 1) / kChunkKeys;
   const int cus = device_cus();
   // when the launch's LDS (attention tile or the select) pins one block per
   // CU, fill the CUs the attention leaves; a plain scan: two blocks per CU
-  const long target = big_lds ? std::max<long>(cus - att_blocks, cus / 2) : 2L * cus;
+  long target = big_lds ? std::max<long>(cus - att_blocks, cus / 2) : 2L * cus;
+  if (g_scan_blocks_cap > 0) target = std::min<long>(target, g_scan_blocks_cap);
   long per_row = (target + B - 1) / B;
   per_row = std::min(per_row, std::max(1L, cap_chunks / kMainWaves));
   return (int)std::max(1L, per_row);

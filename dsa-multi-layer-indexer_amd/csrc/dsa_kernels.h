@@ -47,6 +47,7 @@ hipError_t launch_decode_main(const AttnArgs* A, int B_att, const ScanArgs* S, i
                               hipStream_t s);
 void set_scan_variant(int v);
 void set_coop_select(int on);
+void set_scan_blocks_cap(int n);
 int group_wait_timeouts(int reset);
 int attn_auto_nsplit(int topk);
 size_t attn_workspace_bytes(int B, int H, int nsplit);
