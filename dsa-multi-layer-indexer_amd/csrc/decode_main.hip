@@ -41,7 +41,7 @@
 // product (A = query heads, B = key chunk, loaded straight from HBM into
 // registers with the same lane->k assignment as A).  Each lane ends with one
 // key x 4 heads: ReLU*w summed in-lane, then across lane groups with two xor
-// shuffles.  Up to kScanBatch chunks per wave have loads in flight.
+// shuffles.  Several chunks per wave have loads in flight (scan_batch).
 #include <algorithm>
 
 #include "dsa_common.h"
@@ -66,7 +66,6 @@ struct AttnShared {
   float s[kHG * kTile];                  // scores, log2 domain
   uint16_t p[kHG * kPLd];                // probabilities, bf16
   float m[kHG], l[kHG], alpha[kHG];
-  uint32_t sense;  // the (row, head group) barrier's flag value at launch
 };
 static_assert(kMaxSplit * 3 * kHG * sizeof(float) + kMainThreads * 16 <= sizeof(AttnShared::vt), "merge scratch");
 
@@ -125,7 +124,9 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
   const int lane = t & (kWave - 1);
   const int wv = wave_id();
   const int kr = lane & 15, kc = lane >> 4;
-  if (t == 0) sh.sense = group_sense(A.sync + ((long)b * nhg + hg) * kSyncWords, sp);
+  // the barrier's flag value, read now and used at the barrier (the load's
+  // latency hides under the gather)
+  const uint32_t sense = (t == 0) ? group_sense(A.sync + ((long)b * nhg + hg) * kSyncWords, sp) : 0u;
   const int kps = (A.topk + nsplit - 1) / nsplit;
   const int k0 = min(A.topk, sp * kps), k1 = min(A.topk, k0 + kps);
   const int* idx_row = A.idx + (long)b * A.topk;
@@ -268,7 +269,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
 
   // every split of (row, head group) waits for the others' partials, then
   // merges a 1/nsplit slice of the 16 x 512 outputs
-  group_barrier(A.sync + ((long)b * nhg + hg) * kSyncWords, sp, nsplit, sh.sense);
+  group_barrier(A.sync + ((long)b * nhg + hg) * kSyncWords, sp, nsplit, sense);
   dbg_stamp(dbk, 4);
 
   // log-sum-exp merge (reference combine_kernel K:996-1045):
@@ -372,7 +373,10 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
 // indexer-scan role
 // ======================================================================
 constexpr int kChunkKeys = 16;
-constexpr int kScanBatch = 8;  // chunks per wave with loads in flight
+// chunks per wave with loads in flight: 8 when the scan workgroup owns its
+// CU (the select's LDS); 4 in a plain scan, where two workgroups share a CU
+template <bool SELECT>
+constexpr int scan_batch() { return SELECT ? 8 : 4; }
 constexpr int kHistBins = 4096;
 
 constexpr int kScanMaxPages = 4100;  // page-table entries a workgroup prefetches
@@ -897,7 +901,7 @@ __device__ __forceinline__ v4f qk_fp8(const v8i& qa, const v8i& kb) {
   return acc;
 }
 
-template <int NHG, int VARIANT>
+template <int NHG, int VARIANT, bool SELECT>
 __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, unsigned char* smem) {
   constexpr int kHeads = NHG * 16;
   ScanShared& sh = *reinterpret_cast<ScanShared*>(smem);
@@ -906,36 +910,49 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   const int dbk = blockIdx.x;
   dbg_stamp(dbk, 0);
   const int cap = min(S.slab_stride, S.pt_stride * DSA_PAGE_TOKENS);
+  const int nb = S.blocks_per_row;
+  const int* pt_row = S.page_table + (long)row * S.pt_stride;
+  // The page-table entries of this workgroup's chunks are prefetched with the
+  // query, speculating that the row is full (len == cap, the usual decode
+  // case) so the prefetch need not wait for seq_lens; a shorter row reloads.
+  const int ncap = (cap + kChunkKeys - 1) / kChunkKeys;
+  const int sc0 = (int)((long)ncap * bid / nb), sc1 = (int)((long)ncap * (bid + 1) / nb);
+  const int spg0 = sc0 >> 2;
+  const int snpg = (sc1 > sc0) ? ((sc1 - 1) >> 2) - spg0 + 1 : 0;
+  constexpr int kQ = kHeads * DSA_INDEX_DIM / 16;  // uint4 of the query block
+  const uint4* qsrc = reinterpret_cast<const uint4*>(S.q8 + (long)row * kHeads * DSA_INDEX_DIM);
+  uint4 qv = make_uint4(0, 0, 0, 0);
+  if (t < kQ) qv = qsrc[t];
+  const float wv0 = (t < kHeads) ? S.w[(long)row * kHeads + t] : 0.f;
+  const int spv = (snpg <= kMainThreads && t < snpg) ? pt_row[spg0 + t] : 0;
   const int len = max(0, min(S.seq_lens[row], cap));
   const int nchunks = (len + kChunkKeys - 1) / kChunkKeys;
-  const int nb = S.blocks_per_row;
   const int c0 = (int)((long)nchunks * bid / nb);
   const int c1 = (int)((long)nchunks * (bid + 1) / nb);
-  const int* pt_row = S.page_table + (long)row * S.pt_stride;
-  // this workgroup's page-table entries, prefetched with the query
   const int pg0 = c0 >> 2;
   const int npg = (c1 > c0) ? ((c1 - 1) >> 2) - pg0 + 1 : 0;
   const bool pts_lds = npg <= kScanMaxPages;
   {
-    constexpr int kQ = kHeads * DSA_INDEX_DIM / 16;  // uint4 of the query block
-    const uint4* src = reinterpret_cast<const uint4*>(S.q8 + (long)row * kHeads * DSA_INDEX_DIM);
-    uint4 qv = make_uint4(0, 0, 0, 0);
-    if (t < kQ) qv = src[t];
-    const float wv0 = (t < kHeads) ? S.w[(long)row * kHeads + t] : 0.f;
-    const int pv = (pts_lds && t < npg) ? pt_row[pg0 + t] : 0;
+    const bool spec_ok = nchunks == ncap && snpg <= kMainThreads;  // then pg0, npg == spg0, snpg
     if (t < kQ) reinterpret_cast<uint4*>(sh.qs)[t] = qv;
-    for (int i = t + kMainThreads; i < kQ; i += kMainThreads) reinterpret_cast<uint4*>(sh.qs)[i] = src[i];
+    for (int i = t + kMainThreads; i < kQ; i += kMainThreads) reinterpret_cast<uint4*>(sh.qs)[i] = qsrc[i];
     if (t < kHeads) sh.ws[t] = wv0;
-    if (pts_lds && t < npg) sh.pts[t] = pv;
-    if (pts_lds)
-      for (int i = t + kMainThreads; i < npg; i += kMainThreads) sh.pts[i] = pt_row[pg0 + i];
+    if (pts_lds) {
+      if (spec_ok) {
+        if (t < npg) sh.pts[t] = spv;
+      } else {
+        for (int i = t; i < npg; i += kMainThreads) sh.pts[i] = pt_row[pg0 + i];
+      }
+    }
     if (with_hist)
       for (int i = t; i < kHistBins; i += kMainThreads) sh.hist[i] = 0u;
-    if (S.coop && t < kNumSync) {  // barrier senses: flipped once per use
-      const uint32_t* sync = S.hist + (long)row * S.hist_row_words + row_sync_off(S.slab_stride);
-      reinterpret_cast<CoopShared*>(smem)->sense[t] = group_sense(sync + t * kSyncWords, bid);
-    }
   }
+  // the row barriers' flag values (flipped once per use), read now and
+  // stored for the select after the scan (the loads' latency hides under it)
+  uint32_t sense = 0;
+  if (S.coop && t < kNumSync)
+    sense = group_sense(S.hist + (long)row * S.hist_row_words + row_sync_off(S.slab_stride) + t * kSyncWords,
+                        bid);
   float* srow = S.scores + (long)row * S.slab_stride;
   {  // slab tail past the last scored chunk -> -inf, spread over the row's blocks
     const long tail0 = (long)nchunks * kChunkKeys;
@@ -968,6 +985,7 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   const int n = c1 - c0;
   const int w0 = c0 + (int)((long)n * wv / kMainWaves);
   const int w1 = c0 + (int)((long)n * (wv + 1) / kMainWaves);
+  constexpr int kScanBatch = scan_batch<SELECT>();
   for (int cb = w0; cb < w1; cb += kScanBatch) {
     uint4 kv[kScanBatch][2];
     float ksc[kScanBatch];
@@ -1017,7 +1035,7 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
         if (with_hist && g < len) {
           const uint32_t key = rank_key(v);
           atomicAdd(&sh.hist[key >> 20], 1u);
-          if (S.coop) reinterpret_cast<CoopShared*>(smem)->keys[g - c0 * kChunkKeys] = key;
+          if (SELECT && S.coop) reinterpret_cast<CoopShared*>(smem)->keys[g - c0 * kChunkKeys] = key;
         }
       }
     }
@@ -1025,6 +1043,7 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   dbg_stamp(dbk, 2);
   dbg_stamp_wave(dbk, 5, kMainWaves - 1);
   if (!with_hist) return;
+  if (S.coop && t < kNumSync) reinterpret_cast<CoopShared*>(smem)->sense[t] = sense;
   __syncthreads();
   dbg_stamp(dbk, 6);
   uint32_t* rs = S.hist + (long)row * S.hist_row_words;
@@ -1034,6 +1053,7 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
       if (c) atomicAdd(&rs[i], c);
     }
   dbg_stamp(dbk, 3);
+  if constexpr (!SELECT) return;
   if (!S.next_idx) return;
   if (S.coop) {
     coop_select(*reinterpret_cast<CoopShared*>(smem), smem, S, bid, nb, len, c0 * kChunkKeys,
@@ -1059,21 +1079,32 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
 // ======================================================================
 // the fused launch
 // ======================================================================
-template <int NHG, int VARIANT>
-__global__ __launch_bounds__(kMainThreads) void decode_main_kernel(AttnArgs A, int n_att, ScanArgs S) {
+// ROLES: bit 0 attention workgroups, bit 1 scan workgroups, bit 2 the scan
+// workgroups also select.  Each role set is its own instantiation, so a
+// launch pays only for the registers of the roles it runs (a scan-only
+// launch keeps several workgroups per CU resident).
+constexpr int kRoleAttn = 1, kRoleScan = 2, kRoleSelect = 4;
+
+template <int NHG, int VARIANT, int ROLES>
+__global__ __launch_bounds__(kMainThreads, ROLES == kRoleScan ? 4 : 1) void decode_main_kernel(AttnArgs A, int n_att,
+                                                                                             ScanArgs S) {
   extern __shared__ __align__(16) unsigned char smem[];
   int bid = blockIdx.x;
-  if (bid < n_att) {
-    const int nhg = A.H / kHG;
-    const int sp = bid % A.nsplit;
-    const int hg = (bid / A.nsplit) % nhg;
-    const int b = bid / (A.nsplit * nhg);
-    attention_block(A, b, hg, sp, smem);
-    return;
+  if constexpr ((ROLES & kRoleAttn) != 0) {
+    if (bid < n_att) {
+      const int nhg = A.H / kHG;
+      const int sp = bid % A.nsplit;
+      const int hg = (bid / A.nsplit) % nhg;
+      const int b = bid / (A.nsplit * nhg);
+      attention_block(A, b, hg, sp, smem);
+      return;
+    }
   }
-  bid -= n_att;
-  const int row = bid / S.blocks_per_row;
-  scan_block<NHG, VARIANT>(S, row, bid % S.blocks_per_row, smem);
+  if constexpr ((ROLES & kRoleScan) != 0) {
+    bid -= n_att;
+    const int row = bid / S.blocks_per_row;
+    scan_block<NHG, VARIANT, (ROLES & kRoleSelect) != 0>(S, row, bid % S.blocks_per_row, smem);
+  }
 }
 
 // ---------------------------------------------------------------- host side
@@ -1140,39 +1171,37 @@ int scan_blocks_per_row(int B, int pt_stride, int slab_stride, int att_blocks, b
   return (int)std::max(1L, per_row);
 }
 
-template <int NHG>
-static hipError_t launch_nhg(dim3 grid, size_t lds, hipStream_t s, const AttnArgs& A, int n_att,
-                             const ScanArgs& S) {
-  if (g_scan_variant == 0)
-    hipLaunchKernelGGL((decode_main_kernel<NHG, 0>), grid, dim3(kMainThreads), lds, s, A, n_att, S);
-  else
-    hipLaunchKernelGGL((decode_main_kernel<NHG, 1>), grid, dim3(kMainThreads), lds, s, A, n_att, S);
+template <int NHG, int VARIANT, int ROLES>
+static hipError_t launch_k(dim3 grid, size_t lds, size_t lds_max, hipStream_t s, const AttnArgs& A,
+                           int n_att, const ScanArgs& S) {
+  static bool attr_set = false;  // one host thread per device (the reference's K:2506-2522 rule)
+  if (!attr_set) {
+    const hipError_t e = hipFuncSetAttribute((const void*)decode_main_kernel<NHG, VARIANT, ROLES>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_max);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((decode_main_kernel<NHG, VARIANT, ROLES>), grid, dim3(kMainThreads), lds, s, A, n_att, S);
   return hipGetLastError();
 }
 
 template <int NHG>
-static hipError_t set_lds_attr(size_t lds) {
-  hipError_t e = hipFuncSetAttribute((const void*)decode_main_kernel<NHG, 0>,
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  if (e != hipSuccess) return e;
-  return hipFuncSetAttribute((const void*)decode_main_kernel<NHG, 1>,
-                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+static hipError_t launch_nhg(dim3 grid, size_t lds, size_t lds_max, hipStream_t s, const AttnArgs& A,
+                             int n_att, const ScanArgs& S) {
+  const bool att = n_att > 0, scan = S.blocks_per_row > 0 && grid.x > (unsigned)n_att;
+  if (!scan) return launch_k<4, 0, kRoleAttn>(grid, lds, lds_max, s, A, n_att, S);
+  if (!att && !S.next_idx)  // plain scan: the only role with the alternative MFMA form
+    return g_scan_variant == 0 ? launch_k<NHG, 0, kRoleScan>(grid, lds, lds_max, s, A, n_att, S)
+                               : launch_k<NHG, 1, kRoleScan>(grid, lds, lds_max, s, A, n_att, S);
+  if (!att) return launch_k<NHG, 0, kRoleScan | kRoleSelect>(grid, lds, lds_max, s, A, n_att, S);
+  return launch_k<NHG, 0, kRoleAttn | kRoleScan | kRoleSelect>(grid, lds, lds_max, s, A, n_att, S);
 }
 
 hipError_t launch_decode_main(const AttnArgs* A, int B_att, const ScanArgs* S, int B_scan,
                               hipStream_t s) {
-  static bool attr_set = false;
   const size_t lds_attn = sizeof(AttnShared);
   const size_t lds_coop = std::max(sizeof(CoopShared), row_select_lds_bytes());
-  if (!attr_set) {
-    const size_t lds_max = std::max(lds_attn, lds_coop);
-    hipError_t e;
-    if ((e = set_lds_attr<1>(lds_max)) != hipSuccess) return e;
-    if ((e = set_lds_attr<2>(lds_max)) != hipSuccess) return e;
-    if ((e = set_lds_attr<3>(lds_max)) != hipSuccess) return e;
-    if ((e = set_lds_attr<4>(lds_max)) != hipSuccess) return e;
-    attr_set = true;
-  }
+  const size_t lds_max = std::max(lds_attn, lds_coop);
   AttnArgs a{};
   ScanArgs sc{};
   int n_att = 0, n_scan = 0;
@@ -1211,10 +1240,10 @@ hipError_t launch_decode_main(const AttnArgs* A, int B_att, const ScanArgs* S, i
   if (select) lds = std::max(lds, sc.coop ? lds_coop : row_select_lds_bytes());
   const dim3 grid(n_att + n_scan);
   switch (S ? sc.Hidx / 16 : 4) {
-    case 1: return launch_nhg<1>(grid, lds, s, a, n_att, sc);
-    case 2: return launch_nhg<2>(grid, lds, s, a, n_att, sc);
-    case 3: return launch_nhg<3>(grid, lds, s, a, n_att, sc);
-    default: return launch_nhg<4>(grid, lds, s, a, n_att, sc);
+    case 1: return launch_nhg<1>(grid, lds, lds_max, s, a, n_att, sc);
+    case 2: return launch_nhg<2>(grid, lds, lds_max, s, a, n_att, sc);
+    case 3: return launch_nhg<3>(grid, lds, lds_max, s, a, n_att, sc);
+    default: return launch_nhg<4>(grid, lds, lds_max, s, a, n_att, sc);
   }
 }
 
