@@ -203,8 +203,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
       float tmax = -INFINITY;
 #pragma unroll
       for (int i = 0; i < 4; ++i) { sv[i] = sh.s[h * kTile + q4 + i]; tmax = fmaxf(tmax, sv[i]); }
-#pragma unroll
-      for (int off = 1; off < 32; off <<= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, off));
+      tmax = half_wave_reduce<2>(tmax);
       const float m_old = sh.m[h];
       const float m_new = fmaxf(m_old, tmax);
       const float alpha = (m_new == -INFINITY) ? 1.f : exp2f(m_old - m_new);
@@ -217,8 +216,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
         psum += p0 + p1;
         pw[i >> 1] = pack_bf16x2(p0, p1);
       }
-#pragma unroll
-      for (int off = 1; off < 32; off <<= 1) psum += __shfl_xor(psum, off);
+      psum = half_wave_reduce<0>(psum);
       uint32_t* prow = reinterpret_cast<uint32_t*>(sh.p + h * kPLd + q4);
       prow[0] = pw[0];
       prow[1] = pw[1];
@@ -499,7 +497,7 @@ __device__ __forceinline__ void coop_select_hist(CoopShared& cs, unsigned char* 
       }
     }
   }
-  const uint4 red = block_sum4(make_uint4(gt, 0, 0, 0), cs.wave_tmp);
+  const uint4 red = block_reduce4<0, 0, 0, 0>(make_uint4(gt, 0, 0, 0), cs.wave_tmp);
   if (t == 0) {
     const uint32_t nmine = cs.misc[0];
     cs.misc[1] = nmine ? atomicAdd(&rs[kCntOff], nmine) : 0u;
@@ -570,8 +568,8 @@ __device__ __forceinline__ void coop_select_hist(CoopShared& cs, unsigned char* 
     acc.w += (k == tstar && before) ? 1u : 0u;
     c_gt_all += g ? 1u : 0u;
   }
-  const uint4 r1 = block_sum4(acc, cs.wave_tmp);
-  const uint4 r2 = block_sum4(make_uint4(c_gt_all, 0, 0, 0), cs.wave_tmp);
+  const uint4 r1 = block_reduce4<0, 0, 0, 0>(acc, cs.wave_tmp);
+  const uint4 r2 = block_reduce4<0, 0, 0, 0>(make_uint4(c_gt_all, 0, 0, 0), cs.wave_tmp);
   const uint32_t ties_before = r1.w;
   const uint32_t base = r1.x + r1.z + (tfin ? min(ties_before, need3) : 0u);
   const uint32_t nsel = r1.y + r2.x + (tfin ? need3 : 0u);
@@ -758,6 +756,7 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
         atomicAdd(&hist[w >= lo ? (w >> sh) - base : spill], 1u);
       });
       __syncthreads();
+      dbg_stamp(dbk, 12);
       find_threshold_fixed<kNB1, kMainThreads>(hist, (uint32_t)K, cs.wave_tmp, cs.res);
       ok = cs.res[2] >= (uint32_t)K;  // the union holds at least K keys >= lo
       T1 = cs.res[0] + base;          // == t* >> sh

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "dsa_mli.h"
 
 namespace dsa {
@@ -61,6 +63,64 @@ __device__ __forceinline__ void e4m3x4_to_f32(uint32_t w, float* o) {
 
 __device__ __forceinline__ int wave_id() {
   return __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+}
+
+// ---- wave-wide scans and reductions on DPP (row shifts + row broadcasts,
+// no LDS round trip; lanes whose source is outside the row keep `ident`) ----
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v, uint32_t ident) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)ident, (int)v, CTRL, ROW_MASK, 0xf, false);
+}
+// OP: 0 = sum, 1 = min, 2 = max (unsigned)
+template <int OP>
+__device__ __forceinline__ uint32_t u32_op(uint32_t a, uint32_t b) {
+  return OP == 0 ? a + b : (OP == 1 ? (a < b ? a : b) : (a > b ? a : b));
+}
+template <int OP>
+constexpr uint32_t u32_ident() { return OP == 1 ? 0xffffffffu : 0u; }
+// inclusive scan over the wave's 64 lanes (lane order)
+template <int OP = 0>
+__device__ __forceinline__ uint32_t wave_scan_incl(uint32_t v) {
+  constexpr uint32_t id = u32_ident<OP>();
+  v = u32_op<OP>(v, dpp_u32<0x111, 0xf>(v, id));  // row_shr:1
+  v = u32_op<OP>(v, dpp_u32<0x112, 0xf>(v, id));  // row_shr:2
+  v = u32_op<OP>(v, dpp_u32<0x114, 0xf>(v, id));  // row_shr:4
+  v = u32_op<OP>(v, dpp_u32<0x118, 0xf>(v, id));  // row_shr:8
+  v = u32_op<OP>(v, dpp_u32<0x142, 0xa>(v, id));  // row_bcast:15 -> rows 1, 3
+  v = u32_op<OP>(v, dpp_u32<0x143, 0xc>(v, id));  // row_bcast:31 -> rows 2, 3
+  return v;
+}
+// reduction over the wave, the same value in every lane
+template <int OP = 0>
+__device__ __forceinline__ uint32_t wave_reduce(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)wave_scan_incl<OP>(v), 63);
+}
+
+// Reductions over each half-wave (lanes 0-31 and 32-63, e.g. one softmax row
+// per half): every lane gets its half's result.  OP: 0 = sum, 2 = max.
+template <int OP>
+__device__ __forceinline__ float half_wave_reduce(float v) {
+  const float id = OP == 2 ? -INFINITY : 0.f;
+  auto op = [](float a, float b) { return OP == 2 ? fmaxf(a, b) : a + b; };
+  auto sh = [&](auto ctrl, auto rows, float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(id), __float_as_int(x), decltype(ctrl)::value,
+                                                      decltype(rows)::value, 0xf, false));
+  };
+  using C1 = std::integral_constant<int, 0x111>;
+  using C2 = std::integral_constant<int, 0x112>;
+  using C4 = std::integral_constant<int, 0x114>;
+  using C8 = std::integral_constant<int, 0x118>;
+  using B15 = std::integral_constant<int, 0x142>;
+  using All = std::integral_constant<int, 0xf>;
+  using Odd = std::integral_constant<int, 0xa>;
+  v = op(v, sh(C1{}, All{}, v));
+  v = op(v, sh(C2{}, All{}, v));
+  v = op(v, sh(C4{}, All{}, v));
+  v = op(v, sh(C8{}, All{}, v));
+  v = op(v, sh(B15{}, Odd{}, v));  // rows 1, 3 += rows 0, 2 (their lane 15)
+  const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+  const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+  return (threadIdx.x & 32) ? hi : lo;
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -179,13 +239,11 @@ __device__ __forceinline__ uint32_t red_op(uint32_t a, uint32_t b) {
 template <int OP0, int OP1, int OP2, int OP3>
 __device__ __forceinline__ uint4 block_reduce4(uint4 v, uint32_t* wave_tmp) {
   const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave, nw = blockDim.x / kWave;
-  for (int o = 32; o >= 1; o >>= 1) {
-    v.x = red_op<OP0>(v.x, __shfl_xor(v.x, o));
-    v.y = red_op<OP1>(v.y, __shfl_xor(v.y, o));
-    v.z = red_op<OP2>(v.z, __shfl_xor(v.z, o));
-    v.w = red_op<OP3>(v.w, __shfl_xor(v.w, o));
-  }
-  if (lane == 0) *reinterpret_cast<uint4*>(&wave_tmp[4 * wv]) = v;
+  v.x = wave_scan_incl<OP0>(v.x);
+  v.y = wave_scan_incl<OP1>(v.y);
+  v.z = wave_scan_incl<OP2>(v.z);
+  v.w = wave_scan_incl<OP3>(v.w);
+  if (lane == kWave - 1) *reinterpret_cast<uint4*>(&wave_tmp[4 * wv]) = v;
   __syncthreads();
   uint4 r = *reinterpret_cast<const uint4*>(&wave_tmp[0]);
   for (int i = 1; i < nw; ++i) {
@@ -194,26 +252,6 @@ __device__ __forceinline__ uint4 block_reduce4(uint4 v, uint32_t* wave_tmp) {
     r.y = red_op<OP1>(r.y, x.y);
     r.z = red_op<OP2>(r.z, x.z);
     r.w = red_op<OP3>(r.w, x.w);
-  }
-  __syncthreads();
-  return r;
-}
-
-// Block-wide sums of four per-thread counts.  wave_tmp: 4 words per wave.
-__device__ __forceinline__ uint4 block_sum4(uint4 v, uint32_t* wave_tmp) {
-  const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave, nw = blockDim.x / kWave;
-  for (int o = 32; o >= 1; o >>= 1) {
-    v.x += __shfl_xor(v.x, o);
-    v.y += __shfl_xor(v.y, o);
-    v.z += __shfl_xor(v.z, o);
-    v.w += __shfl_xor(v.w, o);
-  }
-  if (lane == 0) *reinterpret_cast<uint4*>(&wave_tmp[4 * wv]) = v;
-  __syncthreads();
-  uint4 r = make_uint4(0, 0, 0, 0);
-  for (int i = 0; i < nw; ++i) {
-    const uint4 x = *reinterpret_cast<const uint4*>(&wave_tmp[4 * i]);
-    r.x += x.x; r.y += x.y; r.z += x.z; r.w += x.w;
   }
   __syncthreads();
   return r;

@@ -81,12 +81,7 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* w
   const int lane = threadIdx.x & (kWave - 1);
   const int wv = threadIdx.x / kWave;
   const int nwaves = blockDim.x / kWave;
-  uint32_t inc = v;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const uint32_t n = __shfl_up(inc, o);
-    if (lane >= o) inc += n;
-  }
+  const uint32_t inc = wave_scan_incl(v);
   if (lane == kWave - 1) wave_tmp[wv] = inc;
   __syncthreads();
   uint32_t before = 0, tot = 0;
@@ -362,11 +357,11 @@ __device__ __forceinline__ void take_lowest_ties(FinShared& sh, int nw, uint32_t
 // (finite scores only unless keep) and the bin-T1 candidate list.  Each
 // wave reads 64 consecutive scores per load (256 coalesced bytes) so one
 // ballot is two bitmap words; lane j keeps the ballot of iteration j and
-// the wave stores all 64 ballots with one write per lane.  Candidates are
+// the wave stores its kPassJ ballots with one write per lane.  Candidates are
 // rare (about one score in a hundred): each lane flags its own in a 64-bit
 // mask, a wave prefix sum places them, one LDS atomic per wave reserves
 // the space.
-constexpr int kPassJ = 64;  // == kWave: one ballot slot per lane
+constexpr int kPassJ = 32;  // <= kWave: ballot j is kept by lane j
 
 __device__ __forceinline__ void pass_load(float (&v)[kPassJ], __amdgpu_buffer_rsrc_t rsrc, int wbase,
                                           int lane) {
@@ -388,7 +383,8 @@ __device__ __forceinline__ void pass_batch(FinShared& sh, const float (&v)[kPass
     candm |= (uint64_t)(in && bin == T1) << j;
   }
   const int wpos = wbase + lane * kWave;  // iteration `lane`'s first position
-  if (wpos < len) *reinterpret_cast<uint2*>(&sh.sel[wpos >> 5]) = make_uint2((uint32_t)mine, (uint32_t)(mine >> 32));
+  if (lane < kPassJ && wpos < len)
+    *reinterpret_cast<uint2*>(&sh.sel[wpos >> 5]) = make_uint2((uint32_t)mine, (uint32_t)(mine >> 32));
   if (!collect || !__ballot(candm != 0)) return;
   const uint32_t c = (uint32_t)__popcll(candm);
   uint32_t incl = c;
