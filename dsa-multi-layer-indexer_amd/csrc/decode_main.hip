@@ -860,24 +860,43 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
   const uint32_t nsel = r.z + (tfin ? need3 : 0u);
   dbg_stamp(dbk, 14);
 
-  // ---- emit own selections in position order ----
-  uint32_t run_sel = 0, run_tie = ties_before;
-  for (int i0 = 0; i0 < nown; i0 += kMainThreads) {
-    const int i = i0 + t;
-    const bool in = i < nown;
-    const uint32_t k = in ? cs.keys[i] : 0u;
-    const bool tie = in && tfin && k == tstar;
-    uint32_t tie_tot = 0, sel_tot;
-    uint32_t tie_pre = 0;
-    if (__syncthreads_or(tie)) tie_pre = block_flag_scan(tie, cs.wave_tmp, &tie_tot);
-    const bool sel = in && key_is_finite(k) && (all || k > tstar || (tie && run_tie + tie_pre < need3));
-    const uint32_t sel_pre = block_flag_scan(sel, cs.wave_tmp, &sel_tot);
-    if (sel) {
-      const int p = p_lo + i;
-      o[base + run_sel + sel_pre] = pt_row[p >> 6] * DSA_PAGE_TOKENS + (p & (DSA_PAGE_TOKENS - 1));
+  // ---- emit own selections in position order: thread t owns the
+  // contiguous positions [t*per, (t+1)*per) of this workgroup ----
+  const int per = (nown + kMainThreads - 1) / kMainThreads;
+  const int i0 = min(nown, t * per), i1 = min(nown, i0 + per);
+  uint32_t tie_rank = ties_before;  // rank among all ties of this thread's first tie
+  bool has_tie = false;
+  if (tfin)
+    for (int i = i0; i < i1; ++i) has_tie |= cs.keys[i] == tstar;
+  if (__syncthreads_or(has_tie)) {
+    uint32_t nt = 0;
+    for (int i = i0; i < i1; ++i) nt += (cs.keys[i] == tstar) ? 1u : 0u;
+    uint32_t tot;
+    tie_rank += block_exclusive_scan(nt, cs.wave_tmp, &tot);
+  }
+  uint32_t nmine = 0;
+  {
+    uint32_t tr = tie_rank;
+    for (int i = i0; i < i1; ++i) {
+      const uint32_t k = cs.keys[i];
+      const bool tie = tfin && k == tstar;
+      nmine += (key_is_finite(k) && (all || k > tstar || (tie && tr < need3))) ? 1u : 0u;
+      tr += tie ? 1u : 0u;
     }
-    run_sel += sel_tot;
-    run_tie += tie_tot;
+  }
+  uint32_t tot_sel;
+  uint32_t pos = base + block_exclusive_scan(nmine, cs.wave_tmp, &tot_sel);
+  {
+    uint32_t tr = tie_rank;
+    for (int i = i0; i < i1; ++i) {
+      const uint32_t k = cs.keys[i];
+      const bool tie = tfin && k == tstar;
+      if (key_is_finite(k) && (all || k > tstar || (tie && tr < need3))) {
+        const int p = p_lo + i;
+        o[pos++] = pt_row[p >> 6] * DSA_PAGE_TOKENS + (p & (DSA_PAGE_TOKENS - 1));
+      }
+      tr += tie ? 1u : 0u;
+    }
   }
   if (bid == nb - 1)
     for (int j = (int)nsel + t; j < K; j += kMainThreads) o[j] = -1;
