@@ -389,7 +389,7 @@ struct ScanShared {
 // positions and takes part in the row's selection.
 constexpr int kCoopKeys = 8192;      // positions per workgroup
 constexpr int kCoopMaxBlocks = 256;  // workgroups per row
-constexpr int kPubHdr = 4;           // list header: count, bound bin, finite count, max key
+constexpr int kPubHdr = 4;           // list header: count, bound key, finite count, max key
 constexpr int kCoopCand = 1024;      // threshold-bin candidates resolved by rank counting
 struct CoopShared {
   ScanShared scan;
@@ -410,12 +410,11 @@ struct CoopShared {
   uint32_t ce[kCoopCand];
 };
 
-// Keys per workgroup list (a multiple of 4): about three times a
-// workgroup's expected share of the K selected keys plus 16, within the
-// area.  A list too short for its workgroup only costs the fallback to the
-// histogram form.
+// Keys per workgroup list (a multiple of 4): twice a workgroup's expected
+// share of the K selected keys plus 8, within the area.  A list too short
+// for its workgroup only costs the fallback to the histogram form.
 __host__ __device__ inline int pub_stride(int nb, int K) {
-  const int want = 3 * ((K + nb - 1) / nb) + 16;
+  const int want = 2 * ((K + nb - 1) / nb) + 8;
   return min((want + 3) & ~3, (kPubWords / nb) & ~3);
 }
 
@@ -610,19 +609,24 @@ __device__ __forceinline__ void coop_select_hist(CoopShared& cs, unsigned char* 
   dbg_stamp(dbk, 12);
 }
 
+// A list bound that lists nothing; a row whose bound it is goes to the
+// histogram form (it cannot hold K keys >= the bound).
+constexpr uint32_t kNoKeys = 0xffffffffu;
+__device__ __forceinline__ uint32_t next_bin_key(uint32_t bin) { return bin >= 4095u ? kNoKeys : (bin + 1u) << 20; }
+
 // Published-list form of the cooperative select (the default).  Each scan
-// workgroup of the row publishes, in its stride of the row's list area,
-// every own key in the 12-bit bins >= its bound bin Bb (at most
-// M = stride - 4 keys; Bb = 0 when it holds at most M keys), zero-padded,
-// after a header {count, Bb, finite count} (header words and padding are
-// below every real key: the smallest, -inf, is 0x007fffff).  After ONE
-// group barrier every workgroup reads all lists and, from them alone,
-// finds the exact K-th key t* of their union and the ties to take.  The
-// union holds every key >= t* of the row exactly when t* >> 20 >= every
-// Bb; the workgroups check that (they all see the same lists, so they
-// agree) and otherwise hand the row to the histogram form.  The offsets
-// follow from the lists of the workgroups before this one; each workgroup
-// then writes its own selected positions (KV slots) in position order.
+// workgroup of the row publishes every own key >= its bound lo_b (at most M
+// keys; lo_b = 0 when it holds at most M), zero-padded, in its stride of the
+// row's list area, and a header {count, lo_b, finite count, max key} (the
+// padding is below every real key: the smallest, -inf, is 0x007fffff).
+// After ONE group barrier every workgroup reads all lists and, from them
+// alone, finds the exact K-th key t* of their union and the ties to take.
+// The union holds every key >= t* of the row when it holds at least K keys
+// >= L = the largest bound (then t* >= L); the workgroups check that (they
+// all see the same lists, so they agree) and otherwise hand the row to the
+// histogram form.  The offsets follow from the lists of the workgroups
+// before this one; each workgroup then writes its own selected positions
+// (KV slots) in position order.
 __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem, const ScanArgs& S, int bid,
                                             int nb, int len, int p_lo, int p_hi, uint32_t* rs,
                                             const float* srow, const int* pt_row, int* o) {
@@ -637,14 +641,40 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
   uint32_t* sync = rs + row_sync_off(S.slab_stride);
   const int dbk = blockIdx.x;
 
-  // ---- own list: every key in bins >= Bb ----
-  uint32_t Bb = 0;
+  // ---- own list: every own key >= lo_b, at most M of them.  lo_b is the
+  // smallest key value with at most M own keys at or above it: the 12-bit
+  // histogram of the scan gives its bin, rank counting over that bin's keys
+  // the exact value (a bin of more than kCoopCand keys: the next bin) ----
+  uint32_t lo_b = 0;
   if (all) {
-    Bb = kNB1;  // nothing to publish but the finite count
+    lo_b = kNoKeys;  // nothing to publish but the finite count
   } else if ((uint32_t)nown > M) {
     find_threshold_fixed<kNB1, kMainThreads>(cs.scan.hist, M, cs.wave_tmp, cs.res);  // own histogram
     const uint32_t Tb = cs.res[0];
-    Bb = (cs.res[1] + cs.scan.hist[Tb] <= M) ? Tb : Tb + 1u;
+    const uint32_t need = M - cs.res[1];
+    const uint32_t cb = cs.scan.hist[Tb];
+    if (cb <= need) {
+      lo_b = Tb << 20;  // the whole bin fits
+    } else if (cb > (uint32_t)kCoopCand) {
+      lo_b = next_bin_key(Tb);
+    } else {
+      if (t == 0) { cs.misc[0] = 0u; cs.misc[1] = 0xffffffffu; }
+      __syncthreads();
+      for (int i = t; i < nown; i += kMainThreads) {
+        const uint32_t k = cs.keys[i];
+        if ((k >> 20) == Tb) cs.ck[atomicAdd(&cs.misc[0], 1u)] = k;
+      }
+      __syncthreads();
+      for (uint32_t j = t; j < cb; j += kMainThreads) {
+        const uint32_t c = cs.ck[j];
+        uint32_t gec = 0;
+        for (uint32_t i = 0; i < cb; ++i) gec += (cs.ck[i] >= c) ? 1u : 0u;
+        if (gec <= need) atomicMin(&cs.misc[1], c);
+      }
+      __syncthreads();
+      // no key of the bin fits (ties at its top): start above the bin
+      lo_b = cs.misc[1] != 0xffffffffu ? cs.misc[1] : next_bin_key(Tb);
+    }
   }
   if (t == 0) cs.misc[0] = 0u;
   __syncthreads();
@@ -652,7 +682,7 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
   for (int i = t; i < nown; i += kMainThreads) {
     const uint32_t k = cs.keys[i];
     nfin += key_is_finite(k) ? 1u : 0u;
-    if ((k >> 20) >= Bb) {
+    if (k >= lo_b && lo_b != kNoKeys) {
       cs.pub[atomicAdd(&cs.misc[0], 1u)] = k;
       kmax_own = max(kmax_own, k);
     }
@@ -665,7 +695,7 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
     if (!all)
       for (int i = t; i < P; i += kMainThreads) store_dev(&mine[i], (uint32_t)i < cnt ? cs.pub[i] : 0u);
     if (t < kPubHdr) {
-      const uint32_t v = t == 0 ? cnt : (t == 1 ? Bb : (t == 2 ? fin_own : own.y));
+      const uint32_t v = t == 0 ? cnt : (t == 1 ? lo_b : (t == 2 ? fin_own : own.y));
       store_dev(&ghdr[bid * kPubHdr + t], v);
     }
   }
@@ -737,12 +767,11 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
     acc.x = (t < bid) ? hdr_f : 0u;
     acc.z = hdr_f;
   } else {
-    // t* must be >= L = (largest list bound) << 20 for the lists to hold
-    // every key >= t*; keys below L never matter.
+    // t* must be >= L = the largest list bound for the lists to hold every
+    // key >= t*; keys below L never matter.
     const uint4 hr = block_reduce4<2, 2, 0, 0>(make_uint4(hdr_b, hdr_m, 0, 0), cs.wave_tmp);
-    const uint32_t maxB = hr.x, hi = hr.y;
-    const uint32_t lo = max(maxB << 20, kKeyNegInf);
-    bool ok = maxB < (uint32_t)kNB1 && hi >= lo;
+    const uint32_t lo = max(hr.x, kKeyNegInf), hi = hr.y;  // hr.x: the largest list bound
+    bool ok = hi >= lo;
     uint32_t T1 = 0, above = 0;
     int sh = 0;
     if (ok) {

@@ -194,8 +194,10 @@ __device__ __forceinline__ void group_barrier(uint32_t* sync, int bid, int nb, u
       last = atomicAdd(&sync[kGroupSyncGroups * kGroupSyncLine], 1u) == ngroups - 1u;
     }
     if (last) {
+      // re-zero the counters for the next launch (each barrier is used once
+      // per launch, and the launch boundary orders these stores before the
+      // next launch's arrivals, so the flags need not wait for them)
       for (int i = 0; i <= kGroupSyncGroups; ++i) store_dev(&sync[i * kGroupSyncLine], 0u);
-      wait_mem();
       for (int f = 0; f < kGroupSyncFlags; ++f)
         store_dev(&sync[(kGroupSyncGroups + 1 + f) * kGroupSyncLine], sense ^ 1u);
     } else {
