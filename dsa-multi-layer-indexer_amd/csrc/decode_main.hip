@@ -1070,8 +1070,12 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc += wr[hg][r] * fmaxf(d[r], 0.f);
         }
-        acc += __shfl_xor(acc, 16);
-        acc += __shfl_xor(acc, 32);
+        // sum the four 16-lane groups into lanes 0-15 with lane swaps (VALU,
+        // no LDS round trip): + lane i+32, then + lane i+16
+        acc += __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(acc), __float_as_uint(acc),
+                                                                false, false)[1]);
+        acc += __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(acc), __float_as_uint(acc),
+                                                                false, false)[1]);
       }
       const int g = c * kChunkKeys + kr;
       if (lane < 16 && g < S.slab_stride) {
