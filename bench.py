@@ -153,6 +153,8 @@ def main() -> int:
     ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--nsplit", type=int, default=0,
+                    help="attention splits per (row, head group); 0 = the library's choice")
     ap.add_argument("--max-sets", type=int, default=64,
                     help="cap on the rotated layer sets (1: no Infinity-Cache defeat)")
     ap.add_argument("--profile-main", action="store_true",
@@ -189,7 +191,8 @@ def main() -> int:
     sets = []
     for k in range(n_sets):
         layers = [S.make_decode_layer(lens, seed=1000 * 3 + 100 * k + i, device=dev, page_table=pt,
-                                      num_pages=num_pages, indexer=(i % cfg["indexer_every"] == 0))
+                                      num_pages=num_pages, indexer=(i % cfg["indexer_every"] == 0),
+                                      nsplit=args.nsplit)
                   for i in range(n_layers)]
         sets.append(layers)
     layers = sets[0]
@@ -289,7 +292,7 @@ def main() -> int:
     topk_fn = rot_layers(lambda L: lambda: ops.topk(L.scores, L.seq_lens, 2048, page_table=L.page_table,
                                                     out=L.next_idx, scratch=L.topk_scratch))
     topk_ms = graph_event_ms(topk_fn, n_graph, torch)
-    attn_fn = rot_layers(lambda L: lambda: ops.sparse_mla_decode(L.q_bf16, L.kv_pool, first,
+    attn_fn = rot_layers(lambda L: lambda: ops.sparse_mla_decode(L.q_bf16, L.kv_pool, first, nsplit=L.nsplit,
                                                                  workspace=L.workspace, out=L.out))
     attn_ms = graph_event_ms(attn_fn, n_graph, torch)
     ab = attn_bytes(B)

@@ -37,6 +37,22 @@ def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+def _nbytes(t: torch.Tensor) -> int:
+    return t.numel() * t.element_size()
+
+
+def _need_bytes(name: str, t: torch.Tensor, nbytes: int) -> None:
+    """The C ABI takes raw pointers: a caller buffer smaller than the
+    library's size function says would be overrun on the device."""
+    if _nbytes(t) < nbytes:
+        raise RuntimeError(f"{name} holds {_nbytes(t)} bytes, the call needs {nbytes}")
+
+
+def _need_shape(name: str, t: torch.Tensor, shape: tuple, dtype) -> None:
+    if tuple(t.shape) != tuple(shape) or t.dtype != dtype or not t.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous {dtype} {tuple(shape)}, got {t.dtype} {tuple(t.shape)}")
+
+
 def indexer_scan(q_fp8: torch.Tensor, w: torch.Tensor, index_k: torch.Tensor,
                  page_table: torch.Tensor, seq_lens: torch.Tensor, slab_stride: int,
                  out: torch.Tensor | None = None) -> torch.Tensor:
@@ -102,6 +118,8 @@ def topk(scores: torch.Tensor, seq_lens: torch.Tensor, k: int, sorted: bool = Fa
     if scratch is None:
         scratch = topk_scratch(B, slab, scores.device)
     _dev(out, scratch)
+    _need_shape("out", out, (B, k), torch.int32)
+    _need_bytes("top-k scratch", scratch, _lib.load().dsa_topk_scratch_bytes(B, slab))
     _lib.call("dsa_topk", scores.data_ptr(), seq_lens.data_ptr(), _ptr(page_table),
               0 if page_table is None else page_table.shape[1], scratch.data_ptr(),
               out.data_ptr(), B, slab, k,
@@ -110,8 +128,8 @@ def topk(scores: torch.Tensor, seq_lens: torch.Tensor, k: int, sorted: bool = Fa
 
 
 def sparse_mla_workspace(B: int, H: int, nsplit: int, device) -> torch.Tensor:
-    """Zero-filled workspace (split partials + arrival counters; every call
-    leaves the counters zero)."""
+    """Zero-filled workspace (split partials + the splits' barriers; every
+    call leaves the barriers ready).  nsplit=0 sizes it for any split count."""
     nbytes = _lib.load().dsa_sparse_mla_workspace_bytes(B, H, nsplit)
     if nbytes == 0:
         raise RuntimeError(f"bad sparse MLA workspace shape B={B} H={H} nsplit={nsplit}")
@@ -143,6 +161,9 @@ def sparse_mla_decode(q: torch.Tensor, kv_pool: torch.Tensor, idx: torch.Tensor,
     if out is None:
         out = torch.empty(B, H, LATENT_DIM, dtype=torch.bfloat16, device=q.device)
     _dev(workspace, out)
+    _need_shape("out", out, (B, H, LATENT_DIM), torch.bfloat16)
+    # sized for this nsplit (nsplit=0, the library's choice: the largest size)
+    _need_bytes("sparse MLA workspace", workspace, _lib.load().dsa_sparse_mla_workspace_bytes(B, H, nsplit))
     _lib.call("dsa_sparse_mla_decode", q.data_ptr(), kv_pool.data_ptr(), kv_pool.shape[0],
               idx.data_ptr(), workspace.data_ptr(), out.data_ptr(), B, H, idx.shape[1], nsplit,
               float(sm_scale), _stream())

@@ -79,3 +79,24 @@ def test_mla_permutation_invariant_and_deterministic(dev):
     case["idx"] = case["idx"][:, ::-1].copy()
     b = _gpu_mla(case, dev)
     assert C.rel_err(b[0], a[0]) < 1e-2
+
+
+def test_undersized_workspace_rejected_before_launch(dev):
+    """The C ABI takes a raw workspace pointer; the host layer checks its size
+    against dsa_sparse_mla_workspace_bytes for the requested nsplit."""
+    from lagged_indexer_dsa_amd import ops
+    from lagged_indexer_dsa_amd._lib import DsaError
+
+    print("[mla] undersized workspace", flush=True)
+    q = torch.zeros(2, 16, 576, dtype=torch.bfloat16, device=dev)
+    rows = torch.zeros(64, 656, dtype=torch.uint8, device=dev)
+    idx = torch.zeros(2, 2048, dtype=torch.int32, device=dev)
+    small = ops.sparse_mla_workspace(2, 16, 8, dev)
+    with pytest.raises((RuntimeError, DsaError)):
+        ops.sparse_mla_decode(q, rows, idx, nsplit=16, workspace=small)
+    with pytest.raises((RuntimeError, DsaError)):
+        ops.sparse_mla_decode(q, rows, idx, workspace=small)   # nsplit=0: largest size
+    with pytest.raises((RuntimeError, DsaError)):
+        ops.sparse_mla_decode(q, rows, idx, nsplit=8, workspace=small,
+                              out=torch.empty(2, 16, 256, dtype=torch.bfloat16, device=dev))
+    torch.cuda.synchronize()

@@ -118,3 +118,17 @@ def test_topk_rejects_bad_args(dev):
         ops.topk(s, l, 5000, sorted=True)
     with pytest.raises(DsaError):
         ops.topk(s, l, 0)
+
+
+def test_topk_undersized_buffers_rejected_before_launch(dev):
+    from lagged_indexer_dsa_amd import ops
+
+    print("[topk] undersized buffers", flush=True)
+    sc = torch.zeros(2, 8192, device=dev)
+    lens = torch.full((2,), 8192, dtype=torch.int32, device=dev)
+    small = ops.topk_scratch(2, 4096, dev)
+    with pytest.raises(RuntimeError):
+        ops.topk(sc, lens, 2048, scratch=small)
+    with pytest.raises(RuntimeError):
+        ops.topk(sc, lens, 2048, out=torch.empty(2, 1024, dtype=torch.int32, device=dev))
+    torch.cuda.synchronize()
