@@ -169,9 +169,12 @@ int enqueue_layer(const dsa_layer_args* a, const int32_t* attend, bool with_inde
   dsa::AttnArgs A{};
   dsa::ScanArgs S{};
   const bool attention = a->q_bf16 != nullptr && attend != nullptr;
+  const bool shared = attention && with_indexer && attend != a->next_idx;  // one launch, both roles
   if (attention)
     A = attn_args(a->q_bf16, a->kv_pool, a->kv_rows, attend, a->workspace, a->out_bf16, a->B,
-                  a->H, a->topk, a->nsplit, a->sm_scale);
+                  a->H, a->topk,
+                  a->nsplit > 0 ? a->nsplit : (shared ? dsa::attn_fused_nsplit(a->topk, a->B, a->H) : 0),
+                  a->sm_scale);
   if (with_indexer)
     S = scan_args(a->q_fp8, a->w, a->index_k, a->num_idx_pages, a->page_table, a->seq_lens,
                   a->scores, a->Hidx, a->pt_stride, a->slab_stride, a->topk_scratch, a->next_idx,

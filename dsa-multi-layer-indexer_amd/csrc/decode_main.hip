@@ -1187,23 +1187,29 @@ static int device_cus() {
 
 int attn_auto_nsplit(int topk) { return std::max(1, std::min(kMaxSplit, (topk + kTile - 1) / kTile)); }
 
-// [partials o | partials (m, l) | pad to 64 words | one group barrier per
-// (row, head group)]
-static size_t attn_partial_words(size_t blocks) {
-  return (blocks * kHG * (DSA_LATENT_DIM + 2) + 63) / 64 * 64;
+// Splits when the attention shares the launch with indexer scans: one
+// 128-key tile per split, but the attention workgroups together take at most
+// about a quarter of the CUs, so a large batch's scans run beside them
+// (measured at 32 ragged requests: 2 splits 180 us/layer, 16 splits 203).
+int attn_fused_nsplit(int topk, int B, int H) {
+  const int groups = std::max(1, B * (H / kHG));
+  return std::max(1, std::min(attn_auto_nsplit(topk), device_cus() / 4 / groups));
 }
 
+// [one group barrier per (row, head group) | partials o | partials (m, l)]:
+// the barriers sit at offsets that do not depend on nsplit, so launches with
+// different split counts can share one workspace (sized for the largest).
 size_t attn_workspace_bytes(int B, int H, int nsplit) {
   const size_t blocks = (size_t)B * (H / kHG) * nsplit;
   const size_t sync = (size_t)B * (H / kHG) * kSyncWords;
-  return (attn_partial_words(blocks) + sync) * sizeof(float);
+  return (sync + blocks * kHG * (DSA_LATENT_DIM + 2)) * sizeof(float);
 }
 
 void attn_bind_workspace(AttnArgs& A, void* ws, int B) {
   const size_t blocks = (size_t)B * (A.H / kHG) * A.nsplit;
-  A.part_o = reinterpret_cast<float*>(ws);
+  A.sync = reinterpret_cast<uint32_t*>(ws);
+  A.part_o = reinterpret_cast<float*>(A.sync + (size_t)B * (A.H / kHG) * kSyncWords);
   A.part_ml = A.part_o + blocks * kHG * DSA_LATENT_DIM;
-  A.sync = reinterpret_cast<uint32_t*>(A.part_o) + attn_partial_words(blocks);
 }
 
 static int g_scan_blocks_cap = 0;  // internal: cap on scan workgroups per launch (0 = none)

@@ -170,6 +170,10 @@ typedef struct dsa_layer_args {
   int B, Hidx, H, topk, nsplit, pt_stride, slab_stride;
   float sm_scale;
 } dsa_layer_args;
+/* nsplit = 0: automatic.  The attention of a layer launch that also scans
+ * (the lagged case) takes one 128-key tile per split, capped so its
+ * workgroups hold about a quarter of the CUs (large batches then scan beside
+ * them); the attention launched alone takes one tile per split. */
 
 int dsa_decode_layer(const dsa_layer_args* args, void* stream);
 

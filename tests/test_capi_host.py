@@ -106,9 +106,8 @@ def test_mla_contract_and_workspace(lib):
     assert f(None, 16, 10, 16, 16, 16, 1, 16, 2048, 0, 0.04, None) == DSA_ERR_INVALID_ARG
     ws = lib.dsa_sparse_mla_workspace_bytes
     sync = (16 + 1 + 8) * 64                                     # one group barrier, words
-    pad64 = lambda w: (w + 63) // 64 * 64
-    assert ws(1, 16, 32) == (pad64(32 * 16 * 514) + sync) * 4    # partials + barrier
-    assert ws(2, 32, 8) == (pad64(2 * 2 * 8 * 16 * 514) + 4 * sync) * 4
+    assert ws(1, 16, 32) == (sync + 32 * 16 * 514) * 4           # barrier + partials
+    assert ws(2, 32, 8) == (4 * sync + 2 * 2 * 8 * 16 * 514) * 4
     assert ws(1, 16, 0) == ws(1, 16, 128)
     assert ws(1, 15, 8) == 0
 

@@ -100,3 +100,25 @@ def test_undersized_workspace_rejected_before_launch(dev):
         ops.sparse_mla_decode(q, rows, idx, nsplit=8, workspace=small,
                               out=torch.empty(2, 16, 256, dtype=torch.bfloat16, device=dev))
     torch.cuda.synchronize()
+
+
+def test_workspace_shared_across_split_counts(dev):
+    """A workspace sized with nsplit=0 serves any nsplit: launches with
+    different split counts may alternate on it (the split barriers sit at
+    fixed offsets), each equal to the same call on a fresh workspace."""
+    from lagged_indexer_dsa_amd import _lib, ops
+
+    print("[mla] shared workspace across nsplit", flush=True)
+    lib = _lib.load()
+    lib.dsa_internal_group_wait_timeouts(1)
+    case = C.latent_case(77, 4000, 3, 16, 2048)
+    q = C.q_bf16_dev(case["q"], dev)
+    rows = torch.from_numpy(case["rows"]).to(dev)
+    idx = torch.from_numpy(case["idx"]).to(dev)
+    shared = ops.sparse_mla_workspace(3, 16, 0, dev)
+    for ns in [16, 2, 16, 5, 1, 16, 2]:
+        got = ops.sparse_mla_decode(q, rows, idx, nsplit=ns, workspace=shared)
+        ref = ops.sparse_mla_decode(q, rows, idx, nsplit=ns)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), ns
+    assert lib.dsa_internal_group_wait_timeouts(1) == 0
