@@ -296,6 +296,27 @@ def main() -> int:
                                                                  workspace=L.workspace, out=L.out))
     attn_ms = graph_event_ms(attn_fn, n_graph, torch)
     ab = attn_bytes(B)
+    # decode-step operand preparation for one layer: quantize the indexer
+    # query, append each row's newest key and latent row (the token at
+    # seq_len - 1, rewritten in place)
+    Lp = L0s[0]
+    gq = torch.Generator(device=dev).manual_seed(11)
+    q_idx = torch.randn(B, 64, 128, generator=gq, device=dev).to(torch.bfloat16)
+    w_idx = torch.randn(B, 64, generator=gq, device=dev) / 8
+    new_k = torch.randn(B, 128, generator=gq, device=dev).to(torch.bfloat16)
+    new_lat = torch.randn(B, 576, generator=gq, device=dev).to(torch.bfloat16)
+    rows_i = torch.arange(B, dtype=torch.int32, device=dev)
+    pos_i = (Lp.seq_lens - 1).to(torch.int32)
+    slot_i = torch.gather(Lp.page_table.long(), 1, (pos_i.long() // 64)[:, None])[:, 0] * 64 + pos_i.long() % 64
+    slot_i = slot_i.to(torch.int32)
+    q8_buf = torch.empty(B, 64, 128, dtype=torch.uint8, device=dev)
+    w8_buf = torch.empty(B, 64, dtype=torch.float32, device=dev)
+
+    def prep():
+        ops.quantize_index_query(q_idx, w_idx, out_q=q8_buf, out_w=w8_buf)
+        ops.append_index_keys(Lp.index_k, Lp.page_table, rows_i, pos_i, new_k)
+        ops.append_latent_rows(Lp.kv_pool, slot_i, new_lat)
+    prep_ms = graph_event_ms(prep, 50, torch)
 
     us_layer = ms_step * 1e3 / n_layers
     layer_gbs = lb / (launch_ms * 1e-3) / 1e9
@@ -322,6 +343,7 @@ def main() -> int:
         "tokens_per_s": round(B / (us_layer * 1e-6), 1),
         "indexer_scan_GBps": round(scan_gbs, 1),
         "layer_launch_us": round(launch_ms * 1e3, 3),
+        "operand_prep_us": round(prep_ms * 1e3, 3),
         "kernel_us": {"indexer_scan": round(scan_ms * 1e3, 3), "topk": round(topk_ms * 1e3, 3),
                       "sparse_mla+combine": round(attn_ms * 1e3, 3),
                       "indexer_scan_event_pairs": round(scan_ms_pairs * 1e3, 3)},

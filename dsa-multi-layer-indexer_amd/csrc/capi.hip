@@ -357,6 +357,40 @@ int dsa_internal_set_scan_variant(int v) {
   return DSA_OK;
 }
 
+int dsa_quantize_index_query(const void* q_bf16, const float* w, void* q_fp8, float* w_fold, int B,
+                             int Hidx, void* stream) {
+  DSA_REQUIRE(q_bf16 && w && q_fp8 && w_fold, DSA_ERR_INVALID_ARG,
+              "dsa_quantize_index_query: null pointer");
+  DSA_REQUIRE(B >= 1 && Hidx >= 1, DSA_ERR_INVALID_ARG,
+              "dsa_quantize_index_query: B and Hidx must be >= 1 (got %d, %d)", B, Hidx);
+  return hip_status(dsa::launch_quant_query(q_bf16, w, q_fp8, w_fold, (long)B * Hidx, (hipStream_t)stream),
+                    "quantize index query");
+}
+
+int dsa_append_index_keys(const void* k_bf16, const int32_t* rows, const int32_t* pos, int n,
+                          const int32_t* page_table, int pt_stride, void* index_k, int64_t num_pages,
+                          void* stream) {
+  DSA_REQUIRE(n >= 0, DSA_ERR_INVALID_ARG, "dsa_append_index_keys: n must be >= 0 (got %d)", n);
+  if (n == 0) return DSA_OK;
+  DSA_REQUIRE(k_bf16 && rows && pos && page_table && index_k, DSA_ERR_INVALID_ARG,
+              "dsa_append_index_keys: null pointer");
+  DSA_REQUIRE(pt_stride >= 1 && num_pages >= 1, DSA_ERR_INVALID_ARG,
+              "dsa_append_index_keys: pt_stride and num_pages must be >= 1");
+  return hip_status(dsa::launch_append_keys(k_bf16, rows, pos, n, page_table, pt_stride, index_k, (long)num_pages,
+                                            (hipStream_t)stream),
+                    "append index keys");
+}
+
+int dsa_append_latent_rows(const void* latent_bf16, const int32_t* slots, int n, void* kv_pool, int64_t kv_rows,
+                           void* stream) {
+  DSA_REQUIRE(n >= 0, DSA_ERR_INVALID_ARG, "dsa_append_latent_rows: n must be >= 0 (got %d)", n);
+  if (n == 0) return DSA_OK;
+  DSA_REQUIRE(latent_bf16 && slots && kv_pool, DSA_ERR_INVALID_ARG, "dsa_append_latent_rows: null pointer");
+  DSA_REQUIRE(kv_rows >= 1, DSA_ERR_INVALID_ARG, "dsa_append_latent_rows: kv_rows must be >= 1");
+  return hip_status(dsa::launch_append_latent(latent_bf16, slots, n, kv_pool, (long)kv_rows, (hipStream_t)stream),
+                    "append latent rows");
+}
+
 }  // extern "C"
 // Internal: choose the cooperative (1, default) or single-workgroup (0)
 // select inside the decode launch; read (and optionally reset) the count of

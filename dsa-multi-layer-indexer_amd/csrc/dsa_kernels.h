@@ -64,4 +64,12 @@ hipError_t launch_topk_select(const float* scores, const int* seq_lens, const in
                               int pt_stride, void* scratch, int* out, int B, int slab, int K,
                               int sorted, int pad, hipStream_t s);
 
+// Decode-step operand preparation (quant.hip).
+hipError_t launch_quant_query(const void* q_bf16, const float* w, void* codes, float* w_out, long rows,
+                              hipStream_t s);
+hipError_t launch_append_keys(const void* k_bf16, const int* rows, const int* pos, int n, const int* page_table,
+                              int pt_stride, void* pages, long num_pages, hipStream_t s);
+hipError_t launch_append_latent(const void* lat_bf16, const int* slots, int n, void* pool, long kv_rows,
+                                hipStream_t s);
+
 }  // namespace dsa

@@ -4,4 +4,5 @@
 // relocatable device code.
 #include "topk.hip"
 #include "decode_main.hip"
+#include "quant.hip"
 #include "capi.hip"

@@ -24,11 +24,16 @@ E4M3_MAX = 448.0
 
 
 def quantize_rowwise(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """Per-row (last dim) e4m3 quantisation -> (uint8 codes, float32 scale)."""
+    """Per-row (last dim) e4m3 quantisation -> (uint8 codes, float32 scale).
+
+    The two fp32 divisions are IEEE-rounded on every device: they are done in
+    float64 and rounded once to float32 (exact for a quotient of two fp32
+    values), since a GPU's fp32 division in torch need not be correctly
+    rounded."""
     x = x.float()
     amax = x.abs().amax(dim=-1, keepdim=True).clamp_min(1e-6)
-    scale = amax / E4M3_MAX
-    q = (x / scale).clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)
+    scale = (amax.double() / E4M3_MAX).float()
+    q = (x.double() / scale.double()).float().clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)
     return q.view(torch.uint8), scale.squeeze(-1)
 
 

@@ -168,3 +168,59 @@ def sparse_mla_decode(q: torch.Tensor, kv_pool: torch.Tensor, idx: torch.Tensor,
               idx.data_ptr(), workspace.data_ptr(), out.data_ptr(), B, H, idx.shape[1], nsplit,
               float(sm_scale), _stream())
     return out
+
+
+# ---- decode-step operand preparation (the inputs the decode layer reads) ----
+
+def quantize_index_query(q: torch.Tensor, w: torch.Tensor, out_q: torch.Tensor | None = None,
+                         out_w: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Indexer query [B, Hidx, 128] bf16 and head weights [B, Hidx] fp32 ->
+    (e4m3 codes uint8 [B, Hidx, 128], folded weights w * scale fp32).
+    Per (token, head): scale = max(amax, 1e-6) / 448 (K:2969-2974, K:2984-2985)."""
+    _dev(q, w)
+    if q.dim() != 3 or q.shape[2] != INDEX_DIM or q.dtype != torch.bfloat16:
+        raise RuntimeError("q must be [B, Hidx, 128] bfloat16")
+    B, H, _ = q.shape
+    _need_shape("w", w, (B, H), torch.float32)
+    if out_q is None:
+        out_q = torch.empty(B, H, INDEX_DIM, dtype=torch.uint8, device=q.device)
+    if out_w is None:
+        out_w = torch.empty(B, H, dtype=torch.float32, device=q.device)
+    _dev(out_q, out_w)
+    _need_shape("out_q", out_q, (B, H, INDEX_DIM), torch.uint8)
+    _need_shape("out_w", out_w, (B, H), torch.float32)
+    _lib.call("dsa_quantize_index_query", q.data_ptr(), w.data_ptr(), out_q.data_ptr(), out_w.data_ptr(),
+              B, H, _stream())
+    return out_q, out_w
+
+
+def append_index_keys(index_k: torch.Tensor, page_table: torch.Tensor, rows: torch.Tensor,
+                      pos: torch.Tensor, keys: torch.Tensor) -> None:
+    """Quantize keys [n, 128] bf16 (per token, e4m3 + fp32 scale) into the
+    paged index cache at token positions pos[i] of rows rows[i] (P:339-342)."""
+    _dev(index_k, page_table, rows, pos, keys)
+    n = keys.shape[0]
+    if keys.dim() != 2 or keys.shape[1] != INDEX_DIM or keys.dtype != torch.bfloat16:
+        raise RuntimeError("keys must be [n, 128] bfloat16")
+    if index_k.dim() != 2 or index_k.shape[1] != INDEX_PAGE_BYTES or index_k.dtype != torch.uint8:
+        raise RuntimeError("index_k must be [pages, 8448] uint8")
+    if page_table.dim() != 2 or page_table.dtype != torch.int32:
+        raise RuntimeError("page_table must be [B, pt_stride] int32")
+    _need_shape("rows", rows, (n,), torch.int32)
+    _need_shape("pos", pos, (n,), torch.int32)
+    _lib.call("dsa_append_index_keys", keys.data_ptr(), rows.data_ptr(), pos.data_ptr(), n,
+              page_table.data_ptr(), page_table.shape[1], index_k.data_ptr(), index_k.shape[0], _stream())
+
+
+def append_latent_rows(kv_pool: torch.Tensor, slots: torch.Tensor, latent: torch.Tensor) -> None:
+    """Pack latent [n, 576] bf16 (512 latent | 64 rope) into 656-byte fp8 rows
+    at KV slots slots[i] (per-128 e4m3 + fp32 scales, bf16 rope; K:1114)."""
+    _dev(kv_pool, slots, latent)
+    n = latent.shape[0]
+    if latent.dim() != 2 or latent.shape[1] != QK_DIM or latent.dtype != torch.bfloat16:
+        raise RuntimeError("latent must be [n, 576] bfloat16")
+    if kv_pool.dim() != 2 or kv_pool.shape[1] != LATENT_ROW_BYTES or kv_pool.dtype != torch.uint8:
+        raise RuntimeError("kv_pool must be [rows, 656] uint8")
+    _need_shape("slots", slots, (n,), torch.int32)
+    _lib.call("dsa_append_latent_rows", latent.data_ptr(), slots.data_ptr(), n, kv_pool.data_ptr(),
+              kv_pool.shape[0], _stream())

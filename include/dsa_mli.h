@@ -197,6 +197,43 @@ int dsa_mli_graph_destroy(dsa_mli_graph* graph);
 int dsa_mli_run_eager(const dsa_layer_args* layers, int num_layers,
                       void* stream);
 
+/*
+ * (6) Decode-step operand preparation: the fp8 quantizers and paged appends
+ * whose outputs (4) consumes.  Rule, per 128-element row (the reference
+ * harness's quantize_e4m3_rowwise, K:2969-2974):
+ *   scale = max(amax, 1e-6) / 448,  code = e4m3_rne(clamp(x / scale, +-448)).
+ *
+ * Indexer query: q [B, Hidx, 128] bf16, w [B, Hidx] fp32 ->
+ *   q_fp8 [B, Hidx, 128] e4m3, w_fold [B, Hidx] = w * scale (per head).
+ * Replaces: the serving act_quant of the indexer query and the q-scale fold
+ * (sglang overlay P:338, P:343; transformer.py:1139-1144), harness
+ * K:2981-2985.
+ */
+int dsa_quantize_index_query(const void* q_bf16, const float* w, void* q_fp8, float* w_fold, int B,
+                             int Hidx, void* stream);
+
+/*
+ * Index-K append: keys k [n, 128] bf16 of tokens (rows[i], pos[i]) -> their
+ * codes at slot pos%64 of page page_table[rows[i]*pt_stride + pos/64] and the
+ * fp32 scale in that page's scale tail.  A token whose page entry is outside
+ * [0, num_pages) is skipped.
+ * Replaces: _store_index_k_cache (sglang overlay P:339-342).
+ */
+int dsa_append_index_keys(const void* k_bf16, const int32_t* rows, const int32_t* pos, int n,
+                          const int32_t* page_table, int pt_stride, void* index_k, int64_t num_pages,
+                          void* stream);
+
+/*
+ * Latent append: latent [n, 576] bf16 (512 latent | 64 rope) -> 656-byte rows
+ * at KV slots slots[i]: 512 e4m3 codes quantized per 128-dim group, the four
+ * fp32 group scales, the 64 rope values as bf16 (the layout of (3)).  A slot
+ * outside [0, kv_rows) is skipped.
+ * Replaces: SGLang v0.5.16's fp8 KV-cache quantizer, which the reference's
+ * kernels read back (dequant K:1181-1197; dequantize_k_cache P:789).
+ */
+int dsa_append_latent_rows(const void* latent_bf16, const int32_t* slots, int n, void* kv_pool, int64_t kv_rows,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -128,3 +128,18 @@ def test_mli_contract(lib):
     assert lib.dsa_mli_run_eager(arr, 1, 16) == DSA_ERR_INVALID_ARG
     assert lib.dsa_mli_graph_create(arr, 0, None, ctypes.byref(h)) == DSA_ERR_INVALID_ARG
     assert lib.dsa_mli_graph_destroy(None) == 0
+
+
+def test_operand_prep_contract(lib):
+    """The decode-step quantizers reject bad arguments before any launch."""
+    from lagged_indexer_dsa_amd._lib import DSA_ERR_INVALID_ARG, DSA_OK
+
+    assert lib.dsa_quantize_index_query(None, 16, 16, 16, 1, 64, None) == DSA_ERR_INVALID_ARG
+    assert lib.dsa_quantize_index_query(16, 16, 16, 16, 0, 64, None) == DSA_ERR_INVALID_ARG
+    assert lib.dsa_append_index_keys(16, 16, 16, -1, 16, 4, 16, 4, None) == DSA_ERR_INVALID_ARG
+    assert lib.dsa_append_index_keys(None, None, None, 0, None, 0, None, 0, None) == DSA_OK  # nothing to do
+    assert lib.dsa_append_index_keys(16, None, 16, 2, 16, 4, 16, 4, None) == DSA_ERR_INVALID_ARG
+    assert lib.dsa_append_index_keys(16, 16, 16, 2, 16, 0, 16, 4, None) == DSA_ERR_INVALID_ARG
+    assert lib.dsa_append_latent_rows(16, None, 2, 16, 8, None) == DSA_ERR_INVALID_ARG
+    assert lib.dsa_append_latent_rows(16, 16, 2, 16, 0, None) == DSA_ERR_INVALID_ARG
+    assert lib.dsa_append_latent_rows(None, None, 0, None, 0, None) == DSA_OK
