@@ -189,32 +189,65 @@ int enqueue_layer(const dsa_layer_args* a, const int32_t* attend, bool with_inde
 }
 
 // The MLI schedule on one stream: layer i = ONE launch running attention(i)
-// over the carried selection side by side with indexer-scan(i) + top-k(i),
-// whose selection layer i+1's attention consumes.
-int enqueue_mli(const dsa_layer_args* layers, int n, hipStream_t s) {
+// over a lagged selection side by side with indexer-scan(i) + top-k(i).
+// Which selection a layer attends when its attend_idx is NULL (lag depth k,
+// producers R_0, R_1, ... numbered in layer order):
+//   k == 1: the fresh selection of the most recent earlier producer
+//           (P:2942-2997); reuse layers carry that fresh set forward;
+//   k >= 2: producer R_n attends R_{n-k}'s fresh selection once n >= k and the
+//           incoming carry before that; every layer carries out the set it
+//           attended, so reuse layers copy their producer's attended set
+//           (P:1835-1904, P:3020-3100).
+// A layer with attend_idx set attends it, and carries it out unless k == 1
+// and the layer is a producer.
+constexpr int kMaxLagDepth = 64;
+
+template <class F>
+int walk_mli(const dsa_layer_args* layers, int n, int depth, F&& on_layer) {
+  const int32_t* fresh[kMaxLagDepth];  // ring of the last `depth` producers' selections
+  long produced = 0;
   const int32_t* carried = nullptr;
   for (int i = 0; i < n; ++i) {
     const dsa_layer_args* a = &layers[i];
-    const int32_t* att = a->attend_idx ? a->attend_idx : carried;
-    if (a->q_bf16 && !att) return fail(DSA_ERR_INVALID_ARG, "mli layer %d: no selection to attend", i);
-    const int rc = enqueue_layer(a, a->q_bf16 ? att : nullptr, a->q_fp8 != nullptr, s);
+    const bool producer = a->q_fp8 != nullptr;
+    const int32_t* lagged = (producer && depth >= 2 && produced >= depth) ? fresh[produced % depth] : carried;
+    const int32_t* att = a->attend_idx ? a->attend_idx : lagged;
+    const int rc = on_layer(i, a, att);
     if (rc) return rc;
-    if (a->q_fp8) carried = a->next_idx;
+    carried = att;
+    if (producer) {
+      fresh[produced % depth] = a->next_idx;  // the slot just read holds R_{n-k}
+      ++produced;
+      if (depth == 1) carried = a->next_idx;
+    }
   }
   return DSA_OK;
 }
 
-int check_mli(const dsa_layer_args* layers, int n) {
-  DSA_REQUIRE(layers && n >= 1, DSA_ERR_INVALID_ARG, "mli: need at least one layer");
-  const int32_t* carried = nullptr;
-  for (int i = 0; i < n; ++i) {
-    const int rc = check_layer(&layers[i], true);
-    if (rc) return rc;
-    if (layers[i].q_bf16 && !layers[i].attend_idx && !carried)
-      return fail(DSA_ERR_INVALID_ARG, "mli layer %d: attend_idx is NULL and no earlier layer indexes", i);
-    if (layers[i].q_fp8) carried = layers[i].next_idx;
-  }
+int check_depth(int depth) {
+  DSA_REQUIRE(depth >= 1 && depth <= kMaxLagDepth, DSA_ERR_INVALID_ARG, "mli: lag depth %d outside [1, %d]",
+              depth, kMaxLagDepth);
   return DSA_OK;
+}
+
+int enqueue_mli(const dsa_layer_args* layers, int n, int depth, hipStream_t s) {
+  return walk_mli(layers, n, depth, [&](int i, const dsa_layer_args* a, const int32_t* att) {
+    if (a->q_bf16 && !att) return fail(DSA_ERR_INVALID_ARG, "mli layer %d: no selection to attend", i);
+    return enqueue_layer(a, a->q_bf16 ? att : nullptr, a->q_fp8 != nullptr, s);
+  });
+}
+
+int check_mli(const dsa_layer_args* layers, int n, int depth) {
+  DSA_REQUIRE(layers && n >= 1, DSA_ERR_INVALID_ARG, "mli: need at least one layer");
+  int rc = check_depth(depth);
+  if (rc) return rc;
+  return walk_mli(layers, n, depth, [&](int i, const dsa_layer_args* a, const int32_t* att) {
+    const int lrc = check_layer(a, true);
+    if (lrc) return lrc;
+    if (a->q_bf16 && !att)
+      return fail(DSA_ERR_INVALID_ARG, "mli layer %d: attend_idx is NULL and no earlier selection to attend", i);
+    return DSA_OK;
+  });
 }
 
 }  // namespace
@@ -287,17 +320,21 @@ int dsa_decode_layer(const dsa_layer_args* args, void* stream) {
                        (hipStream_t)stream);
 }
 
-int dsa_mli_run_eager(const dsa_layer_args* layers, int num_layers, void* stream) {
-  int rc = check_mli(layers, num_layers);
+int dsa_mli_run_eager_depth(const dsa_layer_args* layers, int num_layers, int lag_depth, void* stream) {
+  int rc = check_mli(layers, num_layers, lag_depth);
   if (rc) return rc;
-  return enqueue_mli(layers, num_layers, (hipStream_t)stream);
+  return enqueue_mli(layers, num_layers, lag_depth, (hipStream_t)stream);
 }
 
-int dsa_mli_graph_create(const dsa_layer_args* layers, int num_layers, void* capture_stream,
-                         dsa_mli_graph** out_graph) {
+int dsa_mli_run_eager(const dsa_layer_args* layers, int num_layers, void* stream) {
+  return dsa_mli_run_eager_depth(layers, num_layers, 1, stream);
+}
+
+int dsa_mli_graph_create_depth(const dsa_layer_args* layers, int num_layers, int lag_depth,
+                               void* capture_stream, dsa_mli_graph** out_graph) {
   DSA_REQUIRE(out_graph, DSA_ERR_INVALID_ARG, "dsa_mli_graph_create: out_graph is null");
   *out_graph = nullptr;
-  int rc = check_mli(layers, num_layers);
+  int rc = check_mli(layers, num_layers, lag_depth);
   if (rc) return rc;
   DSA_REQUIRE(capture_stream, DSA_ERR_INVALID_ARG,
               "dsa_mli_graph_create: capture_stream must be a non-null stream");
@@ -305,7 +342,7 @@ int dsa_mli_graph_create(const dsa_layer_args* layers, int num_layers, void* cap
   dsa_mli_graph* g = new dsa_mli_graph();
   rc = hip_status(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
   if (!rc) {
-    const int erc = enqueue_mli(layers, num_layers, s);
+    const int erc = enqueue_mli(layers, num_layers, lag_depth, s);
     const int crc = hip_status(hipStreamEndCapture(s, &g->graph), "hipStreamEndCapture");
     rc = erc ? erc : crc;
     if (!rc) rc = hip_status(hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0),
@@ -317,6 +354,11 @@ int dsa_mli_graph_create(const dsa_layer_args* layers, int num_layers, void* cap
   }
   *out_graph = g;
   return DSA_OK;
+}
+
+int dsa_mli_graph_create(const dsa_layer_args* layers, int num_layers, void* capture_stream,
+                         dsa_mli_graph** out_graph) {
+  return dsa_mli_graph_create_depth(layers, num_layers, 1, capture_stream, out_graph);
 }
 
 int dsa_mli_graph_launch(dsa_mli_graph* graph, void* stream) {

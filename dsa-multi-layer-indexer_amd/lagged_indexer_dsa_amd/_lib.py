@@ -76,6 +76,8 @@ SIGNATURES = {
     "dsa_mli_graph_launch": (_i32, [_vp, _vp]),
     "dsa_mli_graph_destroy": (_i32, [_vp]),
     "dsa_mli_run_eager": (_i32, [ctypes.POINTER(LayerArgs), _i32, _vp]),
+    "dsa_mli_graph_create_depth": (_i32, [ctypes.POINTER(LayerArgs), _i32, _i32, _vp, ctypes.POINTER(_vp)]),
+    "dsa_mli_run_eager_depth": (_i32, [ctypes.POINTER(LayerArgs), _i32, _i32, _vp]),
     "dsa_quantize_index_query": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _vp]),
     "dsa_append_index_keys": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, _vp, _i64, _vp]),
     "dsa_append_latent_rows": (_i32, [_vp, _vp, _i32, _vp, _i64, _vp]),

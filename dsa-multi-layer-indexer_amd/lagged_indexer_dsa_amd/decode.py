@@ -112,10 +112,16 @@ class MLISchedule:
 
     def __init__(self, layers: list[DecodeLayer], first_attend: torch.Tensor,
                  indexer: bool = True, attention: bool = True,
-                 attend_all_first: bool = False) -> None:
+                 attend_all_first: bool = False, lag_depth: int = 1) -> None:
         """indexer/attention=False drop that half of every layer (timing of
         the other half alone); attend_all_first makes every layer attend
-        ``first_attend`` (attention-only timing with the same gather volume)."""
+        ``first_attend`` (attention-only timing with the same gather volume).
+        lag_depth k (index_reuse_lag_depth, P:4388-4431): indexer layer R_n
+        attends R_{n-k}'s selection once n >= k, else the carried set; pass
+        layers[0].next_idx as first_attend for the reference's cold start."""
+        if not 1 <= int(lag_depth) <= 64:
+            raise ValueError(f"lag_depth must be in [1, 64], got {lag_depth}")
+        self.lag_depth = int(lag_depth)
         self.layers = layers
         self.first_attend = first_attend
         self._args = []
@@ -128,7 +134,7 @@ class MLISchedule:
     def run_eager(self) -> None:
         # every buffer the launches touch is owned by the layers, which this
         # schedule keeps alive (the allocator-safety rule of P:2986-2990)
-        _lib.call("dsa_mli_run_eager", self._arr, len(self._args),
+        _lib.call("dsa_mli_run_eager_depth", self._arr, len(self._args), self.lag_depth,
                   torch.cuda.current_stream().cuda_stream)
 
     def capture(self) -> None:
@@ -137,7 +143,8 @@ class MLISchedule:
             return
         h = ctypes.c_void_p()
         cap = torch.cuda.Stream()
-        _lib.call("dsa_mli_graph_create", self._arr, len(self._args), cap.cuda_stream, ctypes.byref(h))
+        _lib.call("dsa_mli_graph_create_depth", self._arr, len(self._args), self.lag_depth,
+                  cap.cuda_stream, ctypes.byref(h))
         self._graph = h
 
     def replay(self) -> None:
@@ -155,3 +162,32 @@ class MLISchedule:
             self.close()
         except Exception:
             pass
+
+
+def indexcache_pattern(num_layers: int, freq: int | None = 1, pattern: str | None = None,
+                       refresh_layers=None) -> str:
+    """IndexCache retention as an "F"/"S" string (F: the layer runs its
+    indexer; S: it reuses), resolved in the precedence of SGLang's
+    dsa_layer_skips_topk as the overlay extends it (P:191-201):
+      * ``pattern`` (index_topk_pattern): one F/S per layer, layers past its
+        end run their indexer;
+      * ``refresh_layers`` (index_refresh_layers, list or comma string): those
+        layers and layer 0 are F;
+      * ``freq`` (index_topk_freq): 1 in every ``freq`` layers, from layer 0.
+    Layers marked S get no indexer operands in the schedule."""
+    if num_layers < 0:
+        raise ValueError("num_layers must be >= 0")
+    if pattern is not None:
+        bad = set(pattern) - {"F", "S"}
+        if bad:
+            raise ValueError(f"pattern may hold only F and S, got {sorted(bad)}")
+        return "".join("S" if i < len(pattern) and pattern[i] == "S" else "F" for i in range(num_layers))
+    if refresh_layers is not None:
+        if isinstance(refresh_layers, str):
+            refresh_layers = [int(x) for x in refresh_layers.split(",") if x.strip()]
+        full = {int(x) for x in refresh_layers} | {0}
+        return "".join("F" if i in full else "S" for i in range(num_layers))
+    f = 1 if freq is None else int(freq)
+    if f < 1:
+        raise ValueError(f"freq must be >= 1, got {freq}")
+    return "".join("F" if i % f == 0 else "S" for i in range(num_layers))

@@ -198,6 +198,28 @@ int dsa_mli_run_eager(const dsa_layer_args* layers, int num_layers,
                       void* stream);
 
 /*
+ * (5b) The same schedule at lag depth k (1 <= k <= 64; k = 1 is the entries
+ * above).  Number the layers that run an indexer R_0, R_1, ... in order.  A
+ * layer whose attend_idx is NULL attends:
+ *   k == 1: the fresh selection of the most recent earlier R (as above);
+ *   k >= 2: for R_n with n >= k, R_{n-k}'s fresh selection; otherwise (R_n
+ *           with n < k, and every reuse layer) the set the previous layer
+ *           attended.  Reuse layers thus copy their producer's attended set.
+ * Give layer 0 its own next_idx as attend_idx for the reference's cold start
+ * (layer 0 attends its own fresh selection; then R_n attends R_{n-k}).
+ * Every selection is written by an earlier launch on the same stream, so no
+ * event joins are needed; depth changes which buffer each layer reads, not
+ * the launches.
+ * Replaces: the depth-k deferred-indexer FIFO (hh_lag_queue_push /
+ * hh_lag_queue_join_oldest, P:1835-1904) and _hh_lag_refresh_dispatch_depth
+ * (P:3020-3100), configured by index_reuse_lag_depth (P:4388-4431).
+ */
+int dsa_mli_graph_create_depth(const dsa_layer_args* layers, int num_layers, int lag_depth,
+                               void* capture_stream, dsa_mli_graph** out_graph);
+int dsa_mli_run_eager_depth(const dsa_layer_args* layers, int num_layers, int lag_depth,
+                            void* stream);
+
+/*
  * (6) Decode-step operand preparation: the fp8 quantizers and paged appends
  * whose outputs (4) consumes.  Rule, per 128-element row (the reference
  * harness's quantize_e4m3_rowwise, K:2969-2974):

@@ -343,13 +343,66 @@ def lagged_indexer_layers(is_dsa: list[bool]) -> list[bool]:
     return [(i + 1 < n and is_dsa[i + 1]) for i in range(n)]
 
 
-def mli_attend_sources(produces: list[bool], first_attend: int = -1) -> list[int]:
-    """For each layer, the index of the layer whose selection it attends
-    under the lag (the most recent producer strictly before it); the first
-    layer attends ``first_attend`` (an externally supplied set, -1)."""
-    src, last = [], first_attend
+def mli_attend_sources(produces: list[bool], first_attend: int = -1, depth: int = 1) -> list[int]:
+    """For each layer, the index of the layer whose fresh selection it
+    attends; ``first_attend`` (-1: an externally supplied set) is what the
+    first layer attends.
+
+    depth 1 (the certified lag, P:2942-2997): the most recent producer
+    strictly before the layer; reuse layers therefore copy the FRESH set of
+    the producer before them.
+
+    depth k >= 2 (P:1835-1904 queue, P:3020-3100 dispatch), restated as the
+    overlay's FIFO: a producer pushes its fresh set; when the queue already
+    holds k entries it first pops the oldest and attends it, otherwise it
+    attends the incoming carry.  The carry out of every layer is the set it
+    ATTENDED, so reuse layers copy their producer's attended set.
+    """
+    if depth < 1:
+        raise ValueError("depth must be >= 1")
+    src = []
+    if depth == 1:
+        last = first_attend
+        for p in produces:
+            src.append(last)
+            if p:
+                last = len(src) - 1
+        return src
+    queue: list[int] = []
+    carry = first_attend
     for i, p in enumerate(produces):
-        src.append(last)
         if p:
-            last = i
+            if len(queue) >= depth:
+                att = queue.pop(0)
+            else:
+                att = carry
+            queue.append(i)
+            if len(queue) > depth:
+                raise AssertionError("queue overflow")
+        else:
+            att = carry
+        src.append(att)
+        carry = att
     return src
+
+
+def indexcache_produces(num_layers: int, freq: int | None = 1, pattern: str | None = None,
+                        refresh_layers=None) -> list[bool]:
+    """Which layers run their indexer (F) and which reuse (S), in the
+    precedence of SGLang's dsa_layer_skips_topk as the overlay extends it
+    (P:191-201): an explicit ``pattern`` string ("F"/"S" per layer, layers
+    past its end are F); else ``refresh_layers`` (a list, or a comma string,
+    of F layers, layer 0 always F); else uniform retention 1-in-``freq``.
+    The uniform rule (layer % freq == 0, so layer 0 is F) is stock SGLang
+    code that the reference does not vendor: parity unpinned for it."""
+    if pattern is not None:
+        return [not (i < len(pattern) and pattern[i] == "S") for i in range(num_layers)]
+    if refresh_layers is not None:
+        if isinstance(refresh_layers, str):
+            refresh_layers = [int(x) for x in refresh_layers.split(",") if x.strip()]
+        keep = set(refresh_layers) | {0}
+        return [i in keep for i in range(num_layers)]
+    f = 1 if freq is None else int(freq)
+    if f < 1:
+        raise ValueError("freq must be >= 1")
+    return [i % f == 0 for i in range(num_layers)]

@@ -47,3 +47,25 @@ def test_install_rebinds_reference_names():
     assert mod.apply_causal_mask is ac.apply_causal_mask
     assert mod.unrelated == 1
     assert not hasattr(mod, "pad_index")
+
+
+def test_indexcache_pattern_equals_oracle():
+    import json
+    import pathlib
+
+    from lagged_indexer_dsa_amd.decode import indexcache_pattern
+    from oracle import dsa_oracle as O
+
+    g = json.loads((pathlib.Path(__file__).parent / "golden" / "indexcache_patterns.json").read_text())
+    cases = [dict(freq=f) for f in (None, 1, 2, 3, 4, 7)]
+    cases += [dict(refresh_layers=r) for r in ([], [3, 9], "2,4, 60", [0])]
+    cases += [dict(pattern=v["pattern"]) for v in g["patterns"].values()]
+    cases += [dict(pattern="FS", freq=3), dict(pattern="", refresh_layers=[4])]
+    for c in cases:
+        for n in (0, 1, 13, 78):
+            want = "".join("F" if p else "S" for p in O.indexcache_produces(n, **c))
+            assert indexcache_pattern(n, **c) == want, (c, n)
+    with pytest.raises(ValueError):
+        indexcache_pattern(4, pattern="FX")
+    with pytest.raises(ValueError):
+        indexcache_pattern(4, freq=0)

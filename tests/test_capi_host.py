@@ -39,7 +39,8 @@ def test_header_declares_the_hot_path():
     names = _declared_functions()
     for n in ["dsa_indexer_scan", "dsa_topk", "dsa_sparse_mla_decode", "dsa_decode_layer",
               "dsa_mli_graph_create", "dsa_mli_graph_launch", "dsa_mli_graph_destroy",
-              "dsa_mli_run_eager", "dsa_sparse_mla_workspace_bytes", "dsa_last_error"]:
+              "dsa_mli_run_eager", "dsa_mli_run_eager_depth", "dsa_mli_graph_create_depth",
+              "dsa_sparse_mla_workspace_bytes", "dsa_last_error"]:
         assert n in names
 
 
@@ -128,6 +129,13 @@ def test_mli_contract(lib):
     assert lib.dsa_mli_run_eager(arr, 1, 16) == DSA_ERR_INVALID_ARG
     assert lib.dsa_mli_graph_create(arr, 0, None, ctypes.byref(h)) == DSA_ERR_INVALID_ARG
     assert lib.dsa_mli_graph_destroy(None) == 0
+    # lag depth outside [1, 64]
+    arr[0].attend_idx = 16
+    for k in (0, -1, 65):
+        assert lib.dsa_mli_run_eager_depth(arr, 1, k, 16) == DSA_ERR_INVALID_ARG
+        assert b"lag depth" in lib.dsa_last_error()
+        assert lib.dsa_mli_graph_create_depth(arr, 1, k, 16, ctypes.byref(h)) == DSA_ERR_INVALID_ARG
+    assert not h.value
 
 
 def test_operand_prep_contract(lib):

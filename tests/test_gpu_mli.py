@@ -2,9 +2,11 @@
 
 Invariants (the reference's tests/test_equivalence.py:45-64 gate, fused ==
 reference with identical index sets, carried over to streams and graphs):
-  * the two-stream schedule (eager and captured) equals the single-stream
-    serial composition of the same kernels, bitwise, outputs and selections;
+  * the schedule (eager and captured) equals the
+    serial composition of the standalone kernels, bitwise, outputs and selections;
   * layer i attends exactly layer i-1's selection (lag), layer 0 the given set;
+  * at lag depth k and under IndexCache patterns each layer attends the
+    selection the oracle's depth-k FIFO names;
   * replaying the graph with eager work in between reproduces it bitwise;
   * the composite's selection equals the oracle top-k of its own scores,
     mapped to KV slots.
@@ -133,3 +135,40 @@ def test_mli_layer_attends_previous_selection(dev):
     o0 = ops.sparse_mla_decode(layers[0].q_bf16, layers[0].kv_pool, first)
     torch.cuda.synchronize()
     assert _eq(o0, layers[0].out)
+
+
+@pytest.mark.parametrize("depth,pattern,cold", [(1, "FFSFSFF", False), (2, "FFFFFF", True),
+                                                 (2, "FFSFSFFS", False), (3, "FSFFSSFF", True)])
+def test_mli_lag_depth_and_indexcache_pattern(dev, depth, pattern, cold):
+    """Each layer's output equals the standalone attention over the selection
+    the oracle's depth-k FIFO names for it (P:1835-1904, P:3020-3100), eager
+    and in a replayed graph; the selections equal the serial ones."""
+    from lagged_indexer_dsa_amd import ops
+    from lagged_indexer_dsa_amd import synthetic as S
+    from lagged_indexer_dsa_amd.decode import MLISchedule
+
+    print(f"[mli] depth={depth} pattern={pattern} cold={cold}", flush=True)
+    pt, num_pages = S.make_page_table(LENS, seed=1, device=dev)
+    layers = [S.make_decode_layer(LENS, seed=40 + i, device=dev, page_table=pt, num_pages=num_pages,
+                                  indexer=(c == "F"))
+              for i, c in enumerate(pattern)]
+    first = layers[0].next_idx if cold else S.random_selection(LENS, 2048, pt, seed=98, device=dev)
+    src = O.mli_attend_sources([c == "F" for c in pattern], 0 if cold else -1, depth)
+    sched = MLISchedule(layers, first, lag_depth=depth)
+    for mode in ("eager", "graph", "graph"):
+        for L in layers:
+            L.out.zero_(); L.next_idx.fill_(-7)
+        torch.cuda.synchronize()
+        sched.run_eager() if mode == "eager" else sched.replay()
+        outs, sels = _snap(layers)
+        for i, L in enumerate(layers):
+            if L.has_indexer:
+                sc = ops.indexer_scan(L.q_fp8, L.w, L.index_k, L.page_table, L.seq_lens, L.slab_stride)
+                ref_sel = ops.topk(sc, L.seq_lens, L.topk, page_table=L.page_table)
+                torch.cuda.synchronize()
+                assert _eq(sels[i], ref_sel), f"{mode} layer {i} selection"
+            att = first if src[i] == -1 else sels[src[i]]
+            ref = ops.sparse_mla_decode(L.q_bf16, L.kv_pool, att, nsplit=L.nsplit)
+            torch.cuda.synchronize()
+            assert _eq(outs[i], ref), f"{mode} layer {i} attends layer {src[i]}"
+    sched.close()

@@ -344,3 +344,58 @@ def test_lagged_indexer_layers_reference_cases():
     assert O.lagged_indexer_layers([True, False, True]) == [False, True, False]
     assert O.mli_attend_sources([True, True, False]) == [-1, 0, 1]
     assert O.mli_attend_sources([True, False, False, False, True, False]) == [-1, 0, 0, 0, 0, 4]
+
+
+def test_lag_depth_matches_overlay_invariants():
+    """P:3020-3060: with the cold start (R_0 attends its own fresh set),
+    refresh layer R_n attends the set produced k refresh layers back from
+    R_k on, and R_1..R_{k-1} attend the incoming carry (R_0's set)."""
+    for k in range(1, 6):
+        src = O.mli_attend_sources([True] * 12, first_attend=0, depth=k)
+        assert src[0] == 0
+        for n in range(1, 12):
+            assert src[n] == (n - k if n >= k else 0), (k, n)
+    # depth 1 is the certified one-layer lag, whatever the pattern
+    rng = np.random.default_rng(3)
+    for _ in range(50):
+        prod = list(rng.random(15) < 0.4)
+        assert O.mli_attend_sources(prod, depth=1) == O.mli_attend_sources(prod)
+    with pytest.raises(ValueError):
+        O.mli_attend_sources([True], depth=0)
+
+
+def test_lag_depth_with_indexcache_reuse():
+    """Reuse layers copy: the FRESH set of the producer before them at depth
+    1 (P:3050-3052), the producer's ATTENDED set at depth >= 2 (P:3040-3046)."""
+    prod = [True, False, True, False, True, False, True, False]
+    assert O.mli_attend_sources(prod, -1, 1) == [-1, 0, 0, 2, 2, 4, 4, 6]
+    assert O.mli_attend_sources(prod, -1, 2) == [-1, -1, -1, -1, 0, 0, 2, 2]
+    assert O.mli_attend_sources(prod, 0, 2) == [0, 0, 0, 0, 0, 0, 2, 2]
+    # brute force over producers: at depth k every layer attends the fresh
+    # set of the producer k producers before the latest producer at or
+    # before it, clamped to the cold start
+    for k in (2, 3, 4):
+        rng = np.random.default_rng(k)
+        for _ in range(40):
+            prod = [True] + list(rng.random(20) < 0.5)
+            src = O.mli_attend_sources(prod, 0, k)
+            R = [i for i, p in enumerate(prod) if p]
+            for i in range(len(prod)):
+                n = max(j for j, r in enumerate(R) if r <= i)
+                assert src[i] == (R[n - k] if n >= k else 0), (k, i)
+
+
+def test_indexcache_published_patterns_and_precedence():
+    import json
+    import pathlib
+
+    g = json.loads((pathlib.Path(__file__).parent / "golden" / "indexcache_patterns.json").read_text())
+    for v in g["patterns"].values():
+        prod = O.indexcache_produces(g["num_layers"], freq=4, pattern=v["pattern"], refresh_layers=[5])
+        assert sum(prod) == v["full_layers"]          # pattern wins over freq and refresh_layers
+        assert prod[0] and prod[1]
+    assert O.indexcache_produces(5, pattern="FS") == [True, False, True, True, True]
+    assert O.indexcache_produces(6, freq=2, refresh_layers="3, 5") == [True, False, False, True, False, True]
+    assert O.indexcache_produces(6, refresh_layers=[]) == [True] + [False] * 5
+    assert O.indexcache_produces(9, freq=4) == [True, False, False, False, True, False, False, False, True]
+    assert O.indexcache_produces(3, freq=None) == [True] * 3
