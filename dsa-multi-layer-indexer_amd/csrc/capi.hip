@@ -377,6 +377,8 @@ int dsa_mli_graph_destroy(dsa_mli_graph* graph) {
 // Internal (not in the public header): phase timestamps.  on=1 clears and
 // enables, on=0 disables; read copies n words (n <= 512*16) of the table.
 int dsa_internal_debug(int on) {
+  DSA_REQUIRE(!on || dsa::kPhaseStamps, DSA_ERR_INVALID_ARG,
+              "dsa_internal_debug: library built without -DDSA_PHASE_STAMPS");
   const int v = on ? 1 : 0;
   hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(dsa::g_dbg_on), &v, sizeof(v));
   if (e == hipSuccess && on) {

@@ -378,10 +378,22 @@ constexpr int scan_batch() { return SELECT ? 8 : 4; }
 constexpr int kHistBins = 4096;
 
 constexpr int kScanMaxPages = 4100;  // page-table entries a workgroup prefetches
+// Histogram area: 4096 fine bins, 32 spill bins (branch-free updates),
+// then 64 coarse bins (coarse c = fine bins [64c, 64c + 64)) and their 32
+// spill bins.
+// Union histogram of the published-list select: 2048 bins in 64 groups of
+// 32, each group padded to 36 words so that lanes summing one group each
+// read distinct LDS banks.
+constexpr int kUnionBins = 2048;
+constexpr int kUnionGroup = 32, kUnionStride = 36, kUnionWords = kWave * kUnionStride;
+__device__ __forceinline__ uint32_t union_slot(uint32_t b) { return b + (b / kUnionGroup) * (kUnionStride - kUnionGroup); }
+constexpr int kCoarseOff = kHistBins + 64;
+constexpr int kCoarseSpillOff = kCoarseOff + 64;
+constexpr int kHistWords = kCoarseSpillOff + 32;
 struct ScanShared {
   uint8_t qs[64 * DSA_INDEX_DIM];
   float ws[64];
-  uint32_t hist[kHistBins + 64];  // + spill bins for branch-free updates
+  uint32_t hist[kHistWords];
   int pts[kScanMaxPages];
 };
 
@@ -406,15 +418,21 @@ struct CoopShared {
   uint32_t res[4];
   uint32_t misc[4];
   uint32_t sense[kNumSync];
-  uint32_t ck[kCoopCand];  // threshold-bin candidates: key, union entry index
+  alignas(16) uint32_t ck[kCoopCand];  // threshold-bin candidates: key, union entry index
   uint32_t ce[kCoopCand];
+  uint32_t wstat[2 * kMainWaves];  // per wave, from the scan: finite keys, largest key
+  uint32_t hred[2 * kMainWaves];   // per wave: list-header reductions
+  uint32_t pred[2 * kMainWaves];   // per wave: union counts of pass 2
 };
 
-// Keys per workgroup list (a multiple of 4): twice a workgroup's expected
-// share of the K selected keys plus 8, within the area.  A list too short
-// for its workgroup only costs the fallback to the histogram form.
+// Keys a workgroup's list aims to hold: twice its expected share of the K
+// selected keys plus 8.  The list's capacity (a multiple of 4, within the
+// area) adds one more share, so that the threshold bin usually fits whole.
+// A list too short for its workgroup only costs the fallback to the
+// histogram form.
+__host__ __device__ inline int pub_target(int nb, int K) { return 2 * ((K + nb - 1) / nb) + 8; }
 __host__ __device__ inline int pub_stride(int nb, int K) {
-  const int want = 2 * ((K + nb - 1) / nb) + 8;
+  const int want = pub_target(nb, K) + (K + nb - 1) / nb;
   return min((want + 3) & ~3, (kPubWords / nb) & ~3);
 }
 
@@ -614,11 +632,78 @@ __device__ __forceinline__ void coop_select_hist(CoopShared& cs, unsigned char* 
 constexpr uint32_t kNoKeys = 0xffffffffu;
 __device__ __forceinline__ uint32_t next_bin_key(uint32_t bin) { return bin >= 4095u ? kNoKeys : (bin + 1u) << 20; }
 
+// ---- wave-level steps of the published-list select: every wave of the
+// workgroup computes the same result, so no block barrier is needed ----
+
+// The largest fine bin T with #(keys in bins >= T) >= need, over the 4096
+// fine bins and their 64 coarse sums: two DPP scans (coarse, then the 64
+// fine bins of the chosen coarse bin).  need >= 1; when the histogram holds
+// fewer than need keys only `total` is set.
+struct BinThreshold {
+  uint32_t bin, above, cnt, total;  // above: keys in bins > bin; cnt: keys in bin
+};
+__device__ __forceinline__ BinThreshold wave_threshold(const uint32_t* hist, uint32_t need) {
+  const int lane = threadIdx.x & (kWave - 1);
+  BinThreshold r{0u, 0u, 0u, 0u};
+  const uint32_t c = hist[kCoarseOff + kWave - 1 - lane];  // lane 0: the top coarse bin
+  const uint32_t pc = wave_scan_incl<0>(c);                 // keys in coarse bins >= 63 - lane
+  r.total = (uint32_t)__builtin_amdgcn_readlane((int)pc, kWave - 1);
+  if (r.total < need) return r;
+  const int l1 = __builtin_ctzll(__ballot(pc >= need));
+  const uint32_t cbin = (uint32_t)(kWave - 1 - l1);
+  const uint32_t above_c = (uint32_t)__builtin_amdgcn_readlane((int)(pc - c), l1);
+  const uint32_t f = hist[cbin * kWave + kWave - 1 - lane];
+  const uint32_t pf = wave_scan_incl<0>(f) + above_c;
+  const int l2 = __builtin_ctzll(__ballot(pf >= need));
+  r.bin = cbin * kWave + (uint32_t)(kWave - 1 - l2);
+  r.cnt = (uint32_t)__builtin_amdgcn_readlane((int)f, l2);
+  r.above = (uint32_t)__builtin_amdgcn_readlane((int)pf, l2) - r.cnt;
+  return r;
+}
+
+// The same over a histogram of kWave groups of PER bins (PER = 32 or 64),
+// group g at word STRIDE * g, without coarse sums: lane l first sums group
+// 63 - l.
+template <int PER, int STRIDE>
+__device__ __forceinline__ BinThreshold wave_threshold_sum(const uint32_t* hist, uint32_t need) {
+  static_assert((PER == 32 || PER == 64) && STRIDE % 4 == 0 && STRIDE >= PER, "group layout");
+  const int lane = threadIdx.x & (kWave - 1);
+  BinThreshold r{0u, 0u, 0u, 0u};
+  const uint4* p = reinterpret_cast<const uint4*>(hist + STRIDE * (kWave - 1 - lane));
+  uint32_t c = 0;
+#pragma unroll
+  for (int q = 0; q < PER / 4; ++q) {
+    const uint4 v = p[q];
+    c += v.x + v.y + v.z + v.w;
+  }
+  const uint32_t pc = wave_scan_incl<0>(c);
+  r.total = (uint32_t)__builtin_amdgcn_readlane((int)pc, kWave - 1);
+  if (r.total < need) return r;
+  const int l1 = __builtin_ctzll(__ballot(pc >= need));
+  const uint32_t grp = (uint32_t)(kWave - 1 - l1);
+  const uint32_t above_c = (uint32_t)__builtin_amdgcn_readlane((int)(pc - c), l1);
+  const uint32_t f = lane < PER ? hist[grp * STRIDE + PER - 1 - lane] : 0u;
+  const uint32_t pf = wave_scan_incl<0>(f) + above_c;
+  const int l2 = __builtin_ctzll(__ballot(lane < PER && pf >= need));
+  r.bin = grp * PER + (uint32_t)(PER - 1 - l2);
+  r.cnt = (uint32_t)__builtin_amdgcn_readlane((int)f, l2);
+  r.above = (uint32_t)__builtin_amdgcn_readlane((int)pf, l2) - r.cnt;
+  return r;
+}
+
+// this lane's rank among the set lanes of a wave mask
+__device__ __forceinline__ uint32_t lane_rank(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
 // Published-list form of the cooperative select (the default).  Each scan
-// workgroup of the row publishes every own key >= its bound lo_b (at most M
-// keys; lo_b = 0 when it holds at most M), zero-padded, in its stride of the
-// row's list area, and a header {count, lo_b, finite count, max key} (the
-// padding is below every real key: the smallest, -inf, is 0x007fffff).
+// workgroup of the row publishes every own key >= its bound lo_b (at most P
+// keys, the list's capacity; lo_b = 0 when it holds at most P), zero-padded,
+// in its stride of the row's list area, and a header {count, lo_b, finite
+// count, max key} (the padding is below every real key: the smallest, -inf,
+// is 0x007fffff).  lo_b is the lower edge of the 12-bit bin holding the
+// workgroup's M-th key when that whole bin fits, else the exact smallest key
+// value with at most P own keys at or above it.
 // After ONE group barrier every workgroup reads all lists and, from them
 // alone, finds the exact K-th key t* of their union and the ties to take.
 // The union holds every key >= t* of the row when it holds at least K keys
@@ -627,75 +712,107 @@ __device__ __forceinline__ uint32_t next_bin_key(uint32_t bin) { return bin >= 4
 // histogram form.  The offsets follow from the lists of the workgroups
 // before this one; each workgroup then writes its own selected positions
 // (KV slots) in position order.
+// Expects, from the scan: the own keys in cs.keys (position order), their
+// fine and coarse histograms, cs.wstat, and cs.misc[2] == 0.
+// pts: this workgroup's page-table entries from page pg0 on (in LDS) when
+// pts_lds, else the row's page table is read from memory.
 __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem, const ScanArgs& S, int bid,
                                             int nb, int len, int p_lo, int p_hi, uint32_t* rs,
-                                            const float* srow, const int* pt_row, int* o) {
+                                            const float* srow, const int* pt_row, int* o, const int* pts,
+                                            int pg0, bool pts_lds) {
   const int t = threadIdx.x;
+  const int lane = t & (kWave - 1);
+  const int wv = wave_id();
   const int K = S.topk;
   const bool all = len <= K;
   const int nown = max(0, p_hi - p_lo);
   const int P = pub_stride(nb, K);
-  const uint32_t M = (uint32_t)P;
+  const uint32_t M = (uint32_t)min(pub_target(nb, K), P);
   uint32_t* ghdr = rs + row_pub_off(S.slab_stride);  // [nb][kPubHdr]
   uint32_t* gpub = ghdr + kPubHdrWords;              // [nb][P] keys, zero-padded
   uint32_t* sync = rs + row_sync_off(S.slab_stride);
   const int dbk = blockIdx.x;
 
-  // ---- own list: every own key >= lo_b, at most M of them.  lo_b is the
-  // smallest key value with at most M own keys at or above it: the 12-bit
-  // histogram of the scan gives its bin, rank counting over that bin's keys
-  // the exact value (a bin of more than kCoopCand keys: the next bin) ----
-  uint32_t lo_b = 0;
+  uint32_t fin_own = 0, kmax_own = 0;  // reduced per wave by the scan
+#pragma unroll
+  for (int w = 0; w < kMainWaves; ++w) {
+    fin_own += cs.wstat[2 * w];
+    kmax_own = max(kmax_own, cs.wstat[2 * w + 1]);
+  }
+
+  // ---- own bound lo_b and the list's count ----
+  uint32_t lo_b = 0, cnt = 0;
   if (all) {
     lo_b = kNoKeys;  // nothing to publish but the finite count
-  } else if ((uint32_t)nown > M) {
-    find_threshold_fixed<kNB1, kMainThreads>(cs.scan.hist, M, cs.wave_tmp, cs.res);  // own histogram
-    const uint32_t Tb = cs.res[0];
-    const uint32_t need = M - cs.res[1];
-    const uint32_t cb = cs.scan.hist[Tb];
-    if (cb <= need) {
-      lo_b = Tb << 20;  // the whole bin fits
-    } else if (cb > (uint32_t)kCoopCand) {
-      lo_b = next_bin_key(Tb);
+  } else if ((uint32_t)nown <= (uint32_t)P) {
+    cnt = (uint32_t)nown;  // every own key
+  } else {
+    const BinThreshold th = wave_threshold(cs.scan.hist, M);
+    if (th.above + th.cnt <= (uint32_t)P) {
+      lo_b = th.bin << 20;  // the whole bin fits
+      cnt = th.above + th.cnt;
+    } else if (th.cnt > 256u) {
+      lo_b = next_bin_key(th.bin);
+      cnt = th.above;
     } else {
-      if (t == 0) { cs.misc[0] = 0u; cs.misc[1] = 0xffffffffu; }
+      // the bin's keys, then the smallest of them, v, with #{own >= v} <= P
+      // by rank counting (each wave the same)
+      if (t == 0) cs.misc[0] = 0u;
       __syncthreads();
-      for (int i = t; i < nown; i += kMainThreads) {
-        const uint32_t k = cs.keys[i];
-        if ((k >> 20) == Tb) cs.ck[atomicAdd(&cs.misc[0], 1u)] = k;
+      for (int i0 = 0; i0 < nown; i0 += kMainThreads) {
+        const int i = i0 + t;
+        const uint32_t k = i < nown ? cs.keys[i] : 0u;
+        const bool in = i < nown && (k >> 20) == th.bin;
+        const uint64_t m = __ballot(in);
+        if (m) {
+          uint32_t b = 0;
+          if (lane == 0) b = atomicAdd(&cs.misc[0], (uint32_t)__popcll(m));
+          b = (uint32_t)__builtin_amdgcn_readlane((int)b, 0);
+          if (in) cs.ck[b + lane_rank(m)] = k;
+        }
       }
       __syncthreads();
-      for (uint32_t j = t; j < cb; j += kMainThreads) {
-        const uint32_t c = cs.ck[j];
+      const uint32_t cb = th.cnt, room = (uint32_t)P - th.above;
+      uint32_t best = kNoKeys, best_n = 0;
+      for (uint32_t j0 = 0; j0 < cb; j0 += kWave) {
+        const uint32_t j = j0 + (uint32_t)lane;
+        const uint32_t c = j < cb ? cs.ck[j] : 0u;
         uint32_t gec = 0;
         for (uint32_t i = 0; i < cb; ++i) gec += (cs.ck[i] >= c) ? 1u : 0u;
-        if (gec <= need) atomicMin(&cs.misc[1], c);
+        const bool valid = j < cb && gec <= room;
+        best = min(best, valid ? c : kNoKeys);
+        best_n = max(best_n, valid ? gec : 0u);
       }
-      __syncthreads();
+      best = wave_reduce<1>(best);
+      best_n = wave_reduce<2>(best_n);
       // no key of the bin fits (ties at its top): start above the bin
-      lo_b = cs.misc[1] != 0xffffffffu ? cs.misc[1] : next_bin_key(Tb);
+      lo_b = best != kNoKeys ? best : next_bin_key(th.bin);
+      cnt = th.above + (best != kNoKeys ? best_n : 0u);
     }
   }
-  if (t == 0) cs.misc[0] = 0u;
-  __syncthreads();
-  uint32_t nfin = 0, kmax_own = 0;
-  for (int i = t; i < nown; i += kMainThreads) {
-    const uint32_t k = cs.keys[i];
-    nfin += key_is_finite(k) ? 1u : 0u;
-    if (k >= lo_b && lo_b != kNoKeys) {
-      cs.pub[atomicAdd(&cs.misc[0], 1u)] = k;
-      kmax_own = max(kmax_own, k);
-    }
-  }
-  const uint4 own = block_reduce4<0, 2, 0, 0>(make_uint4(nfin, kmax_own, 0, 0), cs.wave_tmp);
-  const uint32_t fin_own = own.x;
+
+  // ---- publish: keys straight to the list (slots from one LDS atomic per
+  // wave step; the order inside a list does not matter), zero padding, header
   {
-    const uint32_t cnt = cs.misc[0];
     uint32_t* mine = gpub + (long)bid * P;
+    if (!all && lo_b != kNoKeys) {
+      for (int i0 = 0; i0 < nown; i0 += kMainThreads) {
+        const int i = i0 + t;
+        const uint32_t k = i < nown ? cs.keys[i] : 0u;
+        const bool pub = i < nown && k >= lo_b;
+        const uint64_t m = __ballot(pub);
+        if (m) {
+          uint32_t b = 0;
+          if (lane == 0) b = atomicAdd(&cs.misc[2], (uint32_t)__popcll(m));
+          b = (uint32_t)__builtin_amdgcn_readlane((int)b, 0);
+          if (pub) store_dev(&mine[b + lane_rank(m)], k);
+        }
+      }
+    }
     if (!all)
-      for (int i = t; i < P; i += kMainThreads) store_dev(&mine[i], (uint32_t)i < cnt ? cs.pub[i] : 0u);
+      for (int i = (int)cnt + t; i < P; i += kMainThreads) store_dev(&mine[i], 0u);
     if (t < kPubHdr) {
-      const uint32_t v = t == 0 ? cnt : (t == 1 ? lo_b : (t == 2 ? fin_own : own.y));
+      const uint32_t v = t == 0 ? cnt : (t == 1 ? lo_b : (t == 2 ? fin_own : (cnt ? kmax_own : 0u)));
       store_dev(&ghdr[bid * kPubHdr + t], v);
     }
   }
@@ -703,13 +820,15 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
   group_barrier(sync, bid, nb, cs.sense[0]);
   dbg_stamp(dbk, 9);
 
-  // ---- every workgroup: all lists into LDS (one batch of device-scope
-  // loads), each list's bound bin, finite count and max key ----
+  // ---- every workgroup: all lists into registers (one batch of
+  // device-scope loads; thread t holds uint4s t, t + 512, ... of the area)
+  // and the headers' reductions ----
   const int nent = all ? 0 : nb * P;
   const int n4 = nent >> 2;
-  uint32_t hdr_b = 0, hdr_f = 0, hdr_m = 0;
+  constexpr int kU = kPubWords / 4 / kMainThreads;
+  uint4 u[kU];
   {
-    constexpr int kU = kPubWords / 4 / kMainThreads / 2;  // two batches
+    uint32_t hdr_b = 0, hdr_f = 0, hdr_m = 0;
     const __amdgpu_buffer_rsrc_t r = dev_rsrc(gpub, 4u * (uint32_t)nent);
     if (t < nb) {
       const uint4 h = load_dev16(dev_rsrc(ghdr, 16u * (uint32_t)nb), 16u * t);
@@ -718,78 +837,77 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
       hdr_m = h.w;
     }
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      uint4 u[kU];
-#pragma unroll
-      for (int j = 0; j < kU; ++j) {
-        const int i = t + (h * kU + j) * kMainThreads;
-        if (i < n4) u[j] = load_dev16(r, 16u * i);
-      }
-      if (h == 0)
-        for (int i = t; i < kNB1; i += kMainThreads) cs.scan.hist[i] = 0u;
-#pragma unroll
-      for (int j = 0; j < kU; ++j) {
-        const int i = t + (h * kU + j) * kMainThreads;
-        if (i < n4) reinterpret_cast<uint4*>(cs.pub)[i] = u[j];
-      }
+    for (int j = 0; j < kU; ++j) {
+      const int i = t + j * kMainThreads;
+      u[j] = (j * kMainThreads < n4) ? load_dev16(r, 16u * i) : make_uint4(0, 0, 0, 0);  // 0 past the end
+    }
+    for (int i = t; i < kUnionWords; i += kMainThreads) cs.scan.hist[i] = 0u;
+    if (t < kWave) cs.ck[t] = 0u;  // candidates past the count read as 0
+    // all: (finite keys of the lists before this one, of all lists);
+    // else: (largest bound, largest key)
+    const uint32_t r0 = all ? wave_reduce<0>(t < bid ? hdr_f : 0u) : wave_reduce<2>(hdr_b);
+    const uint32_t r1 = all ? wave_reduce<0>(hdr_f) : wave_reduce<2>(hdr_m);
+    if (lane == 0) {
+      cs.hred[2 * wv] = r0;
+      cs.hred[2 * wv + 1] = r1;
     }
   }
   if (t == 0) cs.misc[1] = 0u;
   __syncthreads();
   dbg_stamp(dbk, 10);
-  // f(word, index) over the union, four uint4 LDS reads in flight per step
-  const auto for_union = [&](auto&& f) {
-    const uint4* p4 = reinterpret_cast<const uint4*>(cs.pub);
-    for (int i0 = t; i0 < n4; i0 += 4 * kMainThreads) {
-      uint4 v[4];
+  uint32_t h0 = 0, h1 = 0;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int i = i0 + q * kMainThreads;
-        v[q] = (i < n4) ? p4[i] : make_uint4(0, 0, 0, 0);
-      }
+  for (int w = 0; w < kMainWaves; ++w) {
+    const uint32_t a = cs.hred[2 * w], b = cs.hred[2 * w + 1];
+    h0 = all ? h0 + a : max(h0, a);
+    h1 = all ? h1 + b : max(h1, b);
+  }
+  // f(word, union index) over this thread's words (zeros past the end: below
+  // every bound)
+  const auto for_mine = [&](auto&& f) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t e = 4u * (uint32_t)(i0 + q * kMainThreads);
-        f(v[q].x, e);
-        f(v[q].y, e + 1u);
-        f(v[q].z, e + 2u);
-        f(v[q].w, e + 3u);
-      }
+    for (int j = 0; j < kU; ++j) {
+      if (j * kMainThreads >= n4) break;  // uniform
+      const uint32_t e = 4u * (uint32_t)(t + j * kMainThreads);
+      f(u[j].x, e);
+      f(u[j].y, e + 1u);
+      f(u[j].z, e + 2u);
+      f(u[j].w, e + 3u);
     }
   };
 
   uint32_t tstar = 0, need3 = 0;
-  // x = selected above t* before this workgroup, y = ties before it,
-  // z = all selected above t*; all: x = finite before, z = all finite
-  uint4 acc = make_uint4(0, 0, 0, 0);
+  // sel_before = selected above t* before this workgroup, ties_before = ties
+  // before it, sel_above = all selected above t*; all: finite counts
+  uint32_t sel_before = 0, ties_before = 0, sel_above = 0;
+  int own_ties = -1;  // this workgroup's keys equal to t*, when known here
   const uint32_t mine0 = (uint32_t)(bid * P);
   if (all) {
-    acc.x = (t < bid) ? hdr_f : 0u;
-    acc.z = hdr_f;
+    sel_before = h0;
+    sel_above = h1;
+    own_ties = 0;
   } else {
     // t* must be >= L = the largest list bound for the lists to hold every
     // key >= t*; keys below L never matter.
-    const uint4 hr = block_reduce4<2, 2, 0, 0>(make_uint4(hdr_b, hdr_m, 0, 0), cs.wave_tmp);
-    const uint32_t lo = max(hr.x, kKeyNegInf), hi = hr.y;  // hr.x: the largest list bound
+    const uint32_t lo = max(h0, kKeyNegInf), hi = h1;
     bool ok = hi >= lo;
-    uint32_t T1 = 0, above = 0;
+    uint32_t T1 = 0, above = 0, nbin = 0;
     int sh = 0;
     if (ok) {
-      // level 1 over the bit window that spreads [lo, hi] over <= 4096 bins
-      while (sh < 32 && (hi >> sh) - (lo >> sh) >= (uint32_t)kNB1) ++sh;
+      // the bit window that spreads [lo, hi] over <= kUnionBins bins
+      while (sh < 32 && (hi >> sh) - (lo >> sh) >= (uint32_t)kUnionBins) ++sh;
       const uint32_t base = lo >> sh;
       uint32_t* hist = cs.scan.hist;
-      // branch-free: keys below lo land in 32 spill bins past the histogram
-      const uint32_t spill = kNB1 + (t & 31);
-      for_union([&](uint32_t w, uint32_t) {
-        atomicAdd(&hist[w >= lo ? (w >> sh) - base : spill], 1u);
-      });
+      // branch-free: keys below lo land in spill bins past the histogram
+      const uint32_t spill = kUnionWords + (t & 31);
+      for_mine([&](uint32_t w, uint32_t) { atomicAdd(&hist[w >= lo ? union_slot((w >> sh) - base) : spill], 1u); });
       __syncthreads();
       dbg_stamp(dbk, 12);
-      find_threshold_fixed<kNB1, kMainThreads>(hist, (uint32_t)K, cs.wave_tmp, cs.res);
-      ok = cs.res[2] >= (uint32_t)K;  // the union holds at least K keys >= lo
-      T1 = cs.res[0] + base;          // == t* >> sh
-      above = cs.res[1];
+      const BinThreshold th = wave_threshold_sum<kUnionGroup, kUnionStride>(hist, (uint32_t)K);
+      ok = th.total >= (uint32_t)K;  // the union holds at least K keys >= lo
+      T1 = th.bin + base;            // == t* >> sh
+      above = th.above;
+      nbin = th.cnt;
     }
     dbg_stamp(dbk, 4);
     if (!ok) {
@@ -798,12 +916,13 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
       return;
     }
     // pass 2: keys above T1's bin count directly; T1's bin -> candidates
-    for_union([&](uint32_t w, uint32_t e) {
+    uint32_t ax = 0, az = 0;
+    for_mine([&](uint32_t w, uint32_t e) {
       const uint32_t bin = w >> sh;
       const bool in = w >= lo;  // also excludes padding
       const uint32_t g = (in && bin > T1 && key_is_finite(w)) ? 1u : 0u;
-      acc.x += (e < mine0) ? g : 0u;
-      acc.z += g;
+      ax += (e < mine0) ? g : 0u;
+      az += g;
       if (in && bin == T1) {
         const uint32_t slot = atomicAdd(&cs.misc[1], 1u);
         if (slot < (uint32_t)kCoopCand) {
@@ -812,81 +931,112 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
         }
       }
     });
+    ax = wave_reduce<0>(ax);
+    az = wave_reduce<0>(az);
+    if (lane == 0) {
+      cs.pred[2 * wv] = ax;
+      cs.pred[2 * wv + 1] = az;
+    }
     __syncthreads();
     dbg_stamp(dbk, 7);
-    const int sh0 = sh;
-    const uint32_t nc = cs.misc[1];
-    const uint32_t need = (uint32_t)K - above;  // 1 <= need <= nc
-    if (nc <= (uint32_t)kCoopCand) {
-      // exact t* by rank counting: the candidate c with
-      // #{> c} < need <= #{>= c}
-      for (uint32_t j = t; j < nc; j += kMainThreads) {
-        const uint32_t c = cs.ck[j];
-        uint32_t gtc = 0, gec = 0;
-        for (uint32_t i = 0; i < nc; ++i) {
-          const uint32_t x = cs.ck[i];
-          gtc += (x > c) ? 1u : 0u;
-          gec += (x >= c) ? 1u : 0u;
-        }
-        if (gtc < need && need <= gec) {
-          cs.res[0] = c;
-          cs.res[1] = need - gtc;
-        }
-      }
-      __syncthreads();
-      tstar = cs.res[0];
-      need3 = cs.res[1];
-    } else {
-      // many keys share T1's bin: refine its low sh bits, <= 10 per level
-      uint32_t* hist = cs.scan.hist;
-      uint32_t prefix = T1, nd = need;
-      while (sh > 0) {
-        const int sub = min(10, sh);
-        sh -= sub;
-        for (int i = t; i < kNB2; i += kMainThreads) hist[i] = 0u;
-        __syncthreads();
-        const int hs = sh + sub;
-        for_union([&](uint32_t w, uint32_t) {
-          if (w >= lo && (w >> hs) == prefix) atomicAdd(&hist[(w >> sh) & ((1u << sub) - 1u)], 1u);
-        });
-        __syncthreads();
-        find_threshold_fixed<kNB2, kMainThreads>(hist, nd, cs.wave_tmp, cs.res);
-        prefix = (prefix << sub) | cs.res[0];
-        nd -= cs.res[1];
-      }
-      tstar = prefix;
-      need3 = nd;
+#pragma unroll
+    for (int w = 0; w < kMainWaves; ++w) {
+      sel_before += cs.pred[2 * w];
+      sel_above += cs.pred[2 * w + 1];
     }
-    dbg_stamp(dbk, 15);
-    // the candidates' share of the offsets
-    if (nc <= (uint32_t)kCoopCand) {
-      for (uint32_t j = t; j < nc; j += kMainThreads) {
-        const uint32_t w = cs.ck[j];
-        const bool g = w > tstar && key_is_finite(w);
-        const bool before = cs.ce[j] < mine0;
-        acc.x += (g && before) ? 1u : 0u;
-        acc.y += (w == tstar && before) ? 1u : 0u;
-        acc.z += g ? 1u : 0u;
+    const uint32_t nc = nbin;                   // == the candidates collected
+    const uint32_t need = (uint32_t)K - above;  // 1 <= need <= nc
+    if (nc <= (uint32_t)kWave) {
+      // each wave: exact t* by rank counting (the candidate c with
+      // #{> c} < need <= #{>= c}) and the candidates' share of the offsets
+      const bool in = lane < (int)nc;
+      const uint32_t c = in ? cs.ck[lane] : 0u;
+      const uint32_t e = in ? cs.ce[lane] : 0u;
+      uint32_t gtc = 0, gec = 0;
+      const uint4* c4 = reinterpret_cast<const uint4*>(cs.ck);  // zero past nc: below every candidate
+      const int nq = ((int)nc + 3) >> 2;
+#pragma unroll 4
+      for (int q = 0; q < nq; ++q) {
+        const uint4 x = c4[q];
+        gtc += (x.x > c ? 1u : 0u) + (x.y > c ? 1u : 0u) + (x.z > c ? 1u : 0u) + (x.w > c ? 1u : 0u);
+        gec += (x.x >= c ? 1u : 0u) + (x.y >= c ? 1u : 0u) + (x.z >= c ? 1u : 0u) + (x.w >= c ? 1u : 0u);
       }
+      const int l = __builtin_ctzll(__ballot(in && gtc < need && need <= gec));
+      tstar = (uint32_t)__builtin_amdgcn_readlane((int)c, l);
+      need3 = need - (uint32_t)__builtin_amdgcn_readlane((int)gtc, l);
+      const bool g = in && c > tstar && key_is_finite(c);
+      const bool tie = in && c == tstar;
+      const bool before = e < mine0;
+      sel_before += (uint32_t)__popcll(__ballot(g && before));
+      ties_before = (uint32_t)__popcll(__ballot(tie && before));
+      sel_above += (uint32_t)__popcll(__ballot(g));
+      own_ties = __popcll(__ballot(tie && e >= mine0 && e < mine0 + (uint32_t)P));
     } else {
-      // the bin-T1 keys' share, from the union (keys above the bin were
-      // counted in pass 2)
-      for_union([&](uint32_t w, uint32_t e) {
-        if (w < lo || (w >> sh0) != T1) return;
+      if (nc <= (uint32_t)kCoopCand) {
+        for (uint32_t j = t; j < nc; j += kMainThreads) {
+          const uint32_t c = cs.ck[j];
+          uint32_t gtc = 0, gec = 0;
+          for (uint32_t i = 0; i < nc; ++i) {
+            const uint32_t x = cs.ck[i];
+            gtc += (x > c) ? 1u : 0u;
+            gec += (x >= c) ? 1u : 0u;
+          }
+          if (gtc < need && need <= gec) {
+            cs.res[0] = c;
+            cs.res[1] = need - gtc;
+          }
+        }
+        __syncthreads();
+        tstar = cs.res[0];
+        need3 = cs.res[1];
+      } else {
+        // many keys share T1's bin: refine its low sh bits, <= 10 per level
+        uint32_t* hist = cs.scan.hist;
+        uint32_t prefix = T1, nd = need;
+        int s2 = sh;
+        while (s2 > 0) {
+          const int sub = min(10, s2);
+          s2 -= sub;
+          for (int i = t; i < kNB2; i += kMainThreads) hist[i] = 0u;
+          __syncthreads();
+          const int hs = s2 + sub;
+          for_mine([&](uint32_t w, uint32_t) {
+            if (w >= lo && (w >> hs) == prefix) atomicAdd(&hist[(w >> s2) & ((1u << sub) - 1u)], 1u);
+          });
+          __syncthreads();
+          find_threshold_fixed<kNB2, kMainThreads>(hist, nd, cs.wave_tmp, cs.res);
+          prefix = (prefix << sub) | cs.res[0];
+          nd -= cs.res[1];
+        }
+        tstar = prefix;
+        need3 = nd;
+      }
+      // the bin-T1 keys' share (keys above the bin were counted in pass 2)
+      uint4 acc = make_uint4(0, 0, 0, 0);
+      const auto count = [&](uint32_t w, uint32_t e) {
         const bool g = w > tstar && key_is_finite(w);
         const bool before = e < mine0;
         acc.x += (g && before) ? 1u : 0u;
         acc.y += (w == tstar && before) ? 1u : 0u;
         acc.z += g ? 1u : 0u;
-      });
+      };
+      if (nc <= (uint32_t)kCoopCand) {
+        for (uint32_t j = t; j < nc; j += kMainThreads) count(cs.ck[j], cs.ce[j]);
+      } else {
+        for_mine([&](uint32_t w, uint32_t e) {
+          if (w >= lo && (w >> sh) == T1) count(w, e);
+        });
+      }
+      const uint4 r = block_reduce4<0, 0, 0, 0>(acc, cs.wave_tmp);
+      sel_before += r.x;
+      ties_before = r.y;
+      sel_above += r.z;
     }
-    dbg_stamp(dbk, 13);
+    dbg_stamp(dbk, 15);
   }
   const bool tfin = !all && key_is_finite(tstar);
-  const uint4 r = block_reduce4<0, 0, 0, 0>(acc, cs.wave_tmp);
-  const uint32_t ties_before = r.y;
-  const uint32_t base = r.x + (tfin ? min(ties_before, need3) : 0u);
-  const uint32_t nsel = r.z + (tfin ? need3 : 0u);
+  const uint32_t base = sel_before + (tfin ? min(ties_before, need3) : 0u);
+  const uint32_t nsel = sel_above + (tfin ? need3 : 0u);
   dbg_stamp(dbk, 14);
 
   // ---- emit own selections in position order: thread t owns the
@@ -894,10 +1044,14 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
   const int per = (nown + kMainThreads - 1) / kMainThreads;
   const int i0 = min(nown, t * per), i1 = min(nown, i0 + per);
   uint32_t tie_rank = ties_before;  // rank among all ties of this thread's first tie
-  bool has_tie = false;
-  if (tfin)
-    for (int i = i0; i < i1; ++i) has_tie |= cs.keys[i] == tstar;
-  if (__syncthreads_or(has_tie)) {
+  bool any_tie = own_ties > 0;
+  if (own_ties < 0) {
+    bool has_tie = false;
+    if (tfin)
+      for (int i = i0; i < i1; ++i) has_tie |= cs.keys[i] == tstar;
+    any_tie = __syncthreads_or(has_tie);
+  }
+  if (tfin && any_tie) {
     uint32_t nt = 0;
     for (int i = i0; i < i1; ++i) nt += (cs.keys[i] == tstar) ? 1u : 0u;
     uint32_t tot;
@@ -922,7 +1076,8 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
       const bool tie = tfin && k == tstar;
       if (key_is_finite(k) && (all || k > tstar || (tie && tr < need3))) {
         const int p = p_lo + i;
-        o[pos++] = pt_row[p >> 6] * DSA_PAGE_TOKENS + (p & (DSA_PAGE_TOKENS - 1));
+        const int page = pts_lds ? pts[(p >> 6) - pg0] : pt_row[p >> 6];
+        o[pos++] = page * DSA_PAGE_TOKENS + (p & (DSA_PAGE_TOKENS - 1));
       }
       tr += tie ? 1u : 0u;
     }
@@ -992,7 +1147,7 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
       }
     }
     if (with_hist)
-      for (int i = t; i < kHistBins; i += kMainThreads) sh.hist[i] = 0u;
+      for (int i = t; i < kHistWords; i += kMainThreads) sh.hist[i] = 0u;
   }
   // the row barriers' flag values (flipped once per use), read now and
   // stored for the select after the scan (the loads' latency hides under it)
@@ -1029,6 +1184,7 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
     for (int r = 0; r < 4; ++r) wr[hg][r] = sh.ws[hg * 16 + 4 * kc + r];
   }
 
+  uint32_t kmax = 0, nfin = 0;  // own keys (cooperative select)
   const int n = c1 - c0;
   const int w0 = c0 + (int)((long)n * wv / kMainWaves);
   const int w1 = c0 + (int)((long)n * (wv + 1) / kMainWaves);
@@ -1086,7 +1242,12 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
         if (with_hist && g < len) {
           const uint32_t key = rank_key(v);
           atomicAdd(&sh.hist[key >> 20], 1u);
-          if (SELECT && S.coop) reinterpret_cast<CoopShared*>(smem)->keys[g - c0 * kChunkKeys] = key;
+          if (SELECT && S.coop) {
+            reinterpret_cast<CoopShared*>(smem)->keys[g - c0 * kChunkKeys] = key;
+            atomicAdd(&sh.hist[kCoarseOff + (key >> 26)], 1u);
+            kmax = max(kmax, key);
+            nfin += key_is_finite(key) ? 1u : 0u;
+          }
         }
       }
     }
@@ -1094,7 +1255,21 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   dbg_stamp(dbk, 2);
   dbg_stamp_wave(dbk, 5, kMainWaves - 1);
   if (!with_hist) return;
-  if (S.coop && t < kNumSync) reinterpret_cast<CoopShared*>(smem)->sense[t] = sense;
+  if constexpr (SELECT) {
+    if (S.coop) {
+      CoopShared& cs = *reinterpret_cast<CoopShared*>(smem);
+      if (t < kNumSync) cs.sense[t] = sense;
+      kmax = wave_reduce<2>(kmax);
+      nfin = wave_reduce<0>(nfin);
+      if (lane == 0) {
+        cs.wstat[2 * wv] = nfin;
+        cs.wstat[2 * wv + 1] = kmax;
+      }
+      if (t == 0) cs.misc[2] = 0u;  // the list's slot counter
+    }
+  } else {
+    if (S.coop && t < kNumSync) reinterpret_cast<CoopShared*>(smem)->sense[t] = sense;
+  }
   __syncthreads();
   dbg_stamp(dbk, 6);
   uint32_t* rs = S.hist + (long)row * S.hist_row_words;
@@ -1108,7 +1283,8 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   if (!S.next_idx) return;
   if (S.coop) {
     coop_select(*reinterpret_cast<CoopShared*>(smem), smem, S, bid, nb, len, c0 * kChunkKeys,
-                min(c1 * kChunkKeys, len), rs, srow, pt_row, S.next_idx + (long)row * S.topk);
+                min(c1 * kChunkKeys, len), rs, srow, pt_row, S.next_idx + (long)row * S.topk, sh.pts, pg0,
+                pts_lds);
     return;
   }
   // arrival: wait for this slice's device-scope score stores and histogram

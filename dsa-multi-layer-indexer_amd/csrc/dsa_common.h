@@ -259,14 +259,18 @@ __device__ __forceinline__ uint4 block_reduce4(uint4 v, uint32_t* wave_tmp) {
   return r;
 }
 
-// Phase timestamps for profiling (off unless enabled through the internal
-// dsa_internal_debug entry point): thread 0 of workgroup `blk` records the
-// 100 MHz constant clock at phase `ph`; one predicated load when off.
+// Phase timestamps for profiling, compiled in only with -DDSA_PHASE_STAMPS
+// (each stamp reads the enable flag from memory and waits for it, which
+// would put a memory round trip on the critical path of every phase):
+// thread 0 of workgroup `blk` records the 100 MHz constant clock at phase
+// `ph` once enabled through the internal dsa_internal_debug entry point.
 // Counterpart of the reference's hp_dbg stamps (K:1076-1091).
 constexpr int kDbgBlocks = 512;
 constexpr int kDbgPhases = 16;
 extern __device__ int g_dbg_on;
 extern __device__ unsigned long long g_dbg[kDbgBlocks * kDbgPhases];
+#ifdef DSA_PHASE_STAMPS
+constexpr bool kPhaseStamps = true;
 __device__ __forceinline__ void dbg_stamp(int blk, int ph) {
   if (g_dbg_on && threadIdx.x == 0 && blk < kDbgBlocks)
     g_dbg[blk * kDbgPhases + ph] = __builtin_amdgcn_s_memrealtime();
@@ -277,5 +281,10 @@ __device__ __forceinline__ void dbg_stamp_wave(int blk, int ph, int w) {
   if (g_dbg_on && threadIdx.x == (unsigned)(w * kWave) && blk < kDbgBlocks)
     g_dbg[blk * kDbgPhases + ph] = __builtin_amdgcn_s_memrealtime();
 }
+#else
+constexpr bool kPhaseStamps = false;
+__device__ __forceinline__ void dbg_stamp(int, int) {}
+__device__ __forceinline__ void dbg_stamp_wave(int, int, int) {}
+#endif
 
 }  // namespace dsa

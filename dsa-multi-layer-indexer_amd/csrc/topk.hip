@@ -548,7 +548,8 @@ __device__ __forceinline__ void finalize_row(FinShared& sh, const float* __restr
     }
     // the ties all carry key t*: in position order they are pads if t* is not finite
     dbg_stamp(blockIdx.y * gridDim.x + blockIdx.x, 13);
-    if (fused && t == 0 && g_dbg_on && blockIdx.x < kDbgBlocks) g_dbg[blockIdx.x * kDbgPhases + 11] = in_bin;
+    if constexpr (kPhaseStamps)
+      if (fused && t == 0 && g_dbg_on && blockIdx.x < kDbgBlocks) g_dbg[blockIdx.x * kDbgPhases + 11] = in_bin;
     if (keep || key_is_finite(tstar)) take_lowest_ties(sh, nw, need3);
   }
   // re-arm the row's histogram and candidate count for the next call (the

@@ -31,16 +31,20 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the DSA HIP library cannot be built")
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every HIP source into LIB_PATH (always recompiles)."""
-    LIB_DIR.mkdir(parents=True, exist_ok=True)
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+def build(verbose: bool = False, out: Path | None = None, phase_stamps: bool = False) -> Path:
+    """Compile every HIP source into LIB_PATH, or `out` (always recompiles).
+    phase_stamps: compile in the per-phase timestamps (profiling builds only;
+    they cost a memory round trip per phase)."""
+    target = Path(out) if out else LIB_PATH
+    target.parent.mkdir(parents=True, exist_ok=True)
+    tmp = target.with_suffix(".so.tmp")
     cmd = [
         hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
         # packed fp32 VALU ops are disabled on purpose (they have produced
         # silent wrong results on this hardware pool)
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         f"-I{INCLUDE}", f"-I{CSRC}",
+        *(["-DDSA_PHASE_STAMPS"] if phase_stamps else []),
         *[str(CSRC / s) for s in SOURCES],
         "-o", str(tmp),
     ]
@@ -49,8 +53,8 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-4000:]}")
     if verbose and res.stderr:
         print(res.stderr, file=sys.stderr)
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, target)
+    return target
 
 
 if __name__ == "__main__":

@@ -9,6 +9,7 @@ loaded (one runtime per process).
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
 import torch  # noqa: F401  (loads torch's HIP runtime before ours)
@@ -89,7 +90,7 @@ def load(path: Path | None = None) -> ctypes.CDLL:
     global _LIB
     if _LIB is not None:
         return _LIB
-    p = Path(path) if path else LIB_PATH
+    p = Path(path) if path else Path(os.environ.get("DSA_MLI_LIB") or LIB_PATH)
     if not p.exists():
         raise RuntimeError(
             f"HIP library {p} is not built: run `python -m lagged_indexer_dsa_amd._build` "
