@@ -195,6 +195,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
     for (int r = 0; r < 4; ++r)
       sh.s[(4 * kc + r) * kTile + kl] = valid ? sacc[r] * A.sm_log2 : -INFINITY;
     __syncthreads();
+    dbg_stamp(dbk, 6);
 
     // online softmax: thread t -> head t/32, keys 4*(t%32) .. +4
     {
@@ -308,20 +309,34 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
       if (t + j * kMainThreads < nsplit * 2 * kHG) mls[t + j * kMainThreads] = v[j];
   }
   __syncthreads();
-  if (t < kHG) {
-    const float* ml = mls + 2 * t;
+  dbg_stamp(dbk, 8);
+  if (t < kHG * 16) {
+    // one 16-lane DPP row per head; lane i of the row takes the splits
+    // i, i + 16, ... (<= kMaxSplit / 16 each)
+    const int h = t >> 4, i = t & 15;
+    constexpr int kPerLane = kMaxSplit / 16;
+    float ms[kPerLane], ls[kPerLane];
     float mx = -INFINITY;
-    for (int s2 = 0; s2 < nsplit; ++s2) mx = fmaxf(mx, ml[s2 * 2 * kHG]);
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+      const int s2 = i + 16 * j;
+      ms[j] = s2 < nsplit ? mls[s2 * 2 * kHG + 2 * h] : -INFINITY;
+      ls[j] = s2 < nsplit ? mls[s2 * 2 * kHG + 2 * h + 1] : 0.f;
+      mx = fmaxf(mx, ms[j]);
+    }
+    mx = row16_reduce<2>(mx);
     float L = 0.f;
-    if (mx != -INFINITY)
-      for (int s2 = 0; s2 < nsplit; ++s2) {
-        const float ms = ml[s2 * 2 * kHG];
-        if (ms != -INFINITY) L += ml[s2 * 2 * kHG + 1] * exp2f(ms - mx);
-      }
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+      ms[j] = ms[j] != -INFINITY ? exp2f(ms[j] - mx) : 0.f;  // the split's factor
+      L += ls[j] * ms[j];
+    }
+    L = row16_reduce<0>(L);
     const float inv = (mx != -INFINITY && L > 0.f) ? 1.f / L : 0.f;
-    for (int s2 = 0; s2 < nsplit; ++s2) {
-      const float ms = ml[s2 * 2 * kHG];
-      wgt[s2 * kHG + t] = (ms != -INFINITY) ? exp2f(ms - mx) * inv : 0.f;
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+      const int s2 = i + 16 * j;
+      if (s2 < nsplit) wgt[s2 * kHG + h] = ms[j] * inv;
     }
   }
   __syncthreads();
@@ -915,22 +930,44 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
       coop_select_hist(cs, smem, S, bid, nb, len, p_lo, p_hi, rs, srow, pt_row, o);
       return;
     }
-    // pass 2: keys above T1's bin count directly; T1's bin -> candidates
-    uint32_t ax = 0, az = 0;
-    for_mine([&](uint32_t w, uint32_t e) {
-      const uint32_t bin = w >> sh;
-      const bool in = w >= lo;  // also excludes padding
-      const uint32_t g = (in && bin > T1 && key_is_finite(w)) ? 1u : 0u;
-      ax += (e < mine0) ? g : 0u;
-      az += g;
-      if (in && bin == T1) {
+    // pass 2: finite keys above T1's bin are selected: count them (and
+    // those of the lists before this one; a list is a whole number of
+    // uint4s); T1's bin -> candidates.  Edges: bin > T1 <=> w > top, and
+    // bin == T1 with w >= lo <=> bot <= w <= top.
+    const uint64_t top64 = (((uint64_t)T1 + 1u) << sh) - 1u;
+    const uint32_t top = top64 > 0xffffffffull ? 0xffffffffu : (uint32_t)top64;
+    const uint32_t bot = max(lo, T1 << sh);
+    uint32_t ax = 0, az = 0, cmask = 0;
+#pragma unroll
+    for (int j = 0; j < kU; ++j) {
+      if (j * kMainThreads >= n4) break;  // uniform
+      const bool before = 4u * (uint32_t)(t + j * kMainThreads) < mine0;
+      const uint32_t w4[4] = {u[j].x, u[j].y, u[j].z, u[j].w};
+      uint32_t gj = 0;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        gj += (w4[c] > top && w4[c] < kKeyPosInf) ? 1u : 0u;
+        cmask |= (w4[c] >= bot && w4[c] <= top) ? (1u << (4 * j + c)) : 0u;
+      }
+      az += gj;
+      ax += before ? gj : 0u;
+    }
+    if (__ballot(cmask != 0)) {  // rare: most waves hold no candidate
+      for (uint32_t m = cmask; m; m &= m - 1u) {
+        const int b = __builtin_ctz(m);
+        const int j = b >> 2, c = b & 3;
+        const uint32_t e = 4u * (uint32_t)(t + j * kMainThreads) + (uint32_t)c;
+        uint32_t w = 0;
+#pragma unroll
+        for (int jj = 0; jj < kU; ++jj)
+          if (jj == j) w = c == 0 ? u[jj].x : (c == 1 ? u[jj].y : (c == 2 ? u[jj].z : u[jj].w));
         const uint32_t slot = atomicAdd(&cs.misc[1], 1u);
         if (slot < (uint32_t)kCoopCand) {
           cs.ck[slot] = w;
           cs.ce[slot] = e;
         }
       }
-    });
+    }
     ax = wave_reduce<0>(ax);
     az = wave_reduce<0>(az);
     if (lane == 0) {

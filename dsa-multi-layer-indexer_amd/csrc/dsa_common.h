@@ -36,16 +36,13 @@ __device__ __forceinline__ bool key_is_finite(uint32_t k) {
   return k > kKeyNegInf && k < kKeyPosInf;
 }
 
-// fp32 -> bf16 bits, round to nearest even (finite and inf inputs; the
-// dequantised values here are never NaN).
-__device__ __forceinline__ uint32_t f32_to_bf16_rn(float f) {
-  uint32_t u = __float_as_uint(f);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
-}
-
+// Two fp32 -> packed bf16 (lo in bits 0-15), round to nearest even: one
+// gfx950 v_cvt_pk_bf16_f32 (the default round mode is nearest even; the
+// inputs here are finite).
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef float v2f __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16_rn(lo) | (f32_to_bf16_rn(hi) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f){lo, hi}, v2bf));
 }
 
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
@@ -121,6 +118,25 @@ __device__ __forceinline__ float half_wave_reduce(float v) {
   const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
   const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
   return (threadIdx.x & 32) ? hi : lo;
+}
+
+// Reduction over each 16-lane DPP row (OP: 0 = sum, 2 = max), every lane
+// of the row gets the result: an inclusive scan by row shifts leaves it in
+// the row's lane 15, which a bpermute hands to the row.  All lanes active.
+template <int OP>
+__device__ __forceinline__ float row16_reduce(float v) {
+  const float id = OP == 2 ? -INFINITY : 0.f;
+  auto op = [](float a, float b) { return OP == 2 ? fmaxf(a, b) : a + b; };
+  auto shr = [&](auto ctrl, float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(id), __float_as_int(x), decltype(ctrl)::value,
+                                                      0xf, 0xf, false));
+  };
+  v = op(v, shr(std::integral_constant<int, 0x111>{}, v));  // row_shr:1
+  v = op(v, shr(std::integral_constant<int, 0x112>{}, v));  // row_shr:2
+  v = op(v, shr(std::integral_constant<int, 0x114>{}, v));  // row_shr:4
+  v = op(v, shr(std::integral_constant<int, 0x118>{}, v));  // row_shr:8 -> lane 15 holds the row's result
+  const int src = (int)((threadIdx.x & ~15u) | 15u) & (kWave - 1);
+  return __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(v)));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -263,22 +279,22 @@ __device__ __forceinline__ uint4 block_reduce4(uint4 v, uint32_t* wave_tmp) {
 // (each stamp reads the enable flag from memory and waits for it, which
 // would put a memory round trip on the critical path of every phase):
 // thread 0 of workgroup `blk` records the 100 MHz constant clock at phase
-// `ph` once enabled through the internal dsa_internal_debug entry point.
+// `ph`; the internal dsa_internal_debug entry point clears the table.
 // Counterpart of the reference's hp_dbg stamps (K:1076-1091).
 constexpr int kDbgBlocks = 512;
 constexpr int kDbgPhases = 16;
 extern __device__ int g_dbg_on;
 extern __device__ unsigned long long g_dbg[kDbgBlocks * kDbgPhases];
 #ifdef DSA_PHASE_STAMPS
+// (profiling builds record unconditionally: a store does not wait)
 constexpr bool kPhaseStamps = true;
 __device__ __forceinline__ void dbg_stamp(int blk, int ph) {
-  if (g_dbg_on && threadIdx.x == 0 && blk < kDbgBlocks)
-    g_dbg[blk * kDbgPhases + ph] = __builtin_amdgcn_s_memrealtime();
+  if (threadIdx.x == 0 && blk < kDbgBlocks) g_dbg[blk * kDbgPhases + ph] = __builtin_amdgcn_s_memrealtime();
 }
 
 // Same, recorded by lane 0 of wave `w` instead of thread 0.
 __device__ __forceinline__ void dbg_stamp_wave(int blk, int ph, int w) {
-  if (g_dbg_on && threadIdx.x == (unsigned)(w * kWave) && blk < kDbgBlocks)
+  if (threadIdx.x == (unsigned)(w * kWave) && blk < kDbgBlocks)
     g_dbg[blk * kDbgPhases + ph] = __builtin_amdgcn_s_memrealtime();
 }
 #else
