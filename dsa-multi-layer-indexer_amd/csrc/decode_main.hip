@@ -952,6 +952,7 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
       az += gj;
       ax += before ? gj : 0u;
     }
+    dbg_stamp(dbk, 13);
     if (__ballot(cmask != 0)) {  // rare: most waves hold no candidate
       for (uint32_t m = cmask; m; m &= m - 1u) {
         const int b = __builtin_ctz(m);
@@ -968,6 +969,7 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
         }
       }
     }
+    dbg_stamp(dbk, 6);
     ax = wave_reduce<0>(ax);
     az = wave_reduce<0>(az);
     if (lane == 0) {
