@@ -984,6 +984,7 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
       sel_above += cs.pred[2 * w + 1];
     }
     const uint32_t nc = nbin;                   // == the candidates collected
+    dbg_value(dbk, 5, ((unsigned long long)nc << 32) | (uint32_t)sh);
     const uint32_t need = (uint32_t)K - above;  // 1 <= need <= nc
     if (nc <= (uint32_t)kWave) {
       // each wave: exact t* by rank counting (the candidate c with
@@ -1228,37 +1229,41 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   const int w0 = c0 + (int)((long)n * wv / kMainWaves);
   const int w1 = c0 + (int)((long)n * (wv + 1) / kMainWaves);
   constexpr int kScanBatch = scan_batch<SELECT>();
-  for (int cb = w0; cb < w1; cb += kScanBatch) {
-    uint4 kv[kScanBatch][2];
-    float ksc[kScanBatch];
-    bool ok[kScanBatch];
-    int page[kScanBatch];
+  // One batch of chunks per step, every load issued before any is used.
+  // Branch-free: each chunk reads through a buffer resource over its page
+  // (an empty one for a chunk past w1 or an invalid page, so its loads
+  // return 0 without a memory access), and the page entries come from LDS,
+  // so the compiler can wait for each chunk's loads alone.  PT_LDS false
+  // (a workgroup with more pages than the LDS table holds; the launcher
+  // sizes workgroups so that this does not happen) reads the page table
+  // from memory instead.
+  const auto run_chunks = [&](auto pt_lds) {
+    constexpr bool kPtLds = decltype(pt_lds)::value;
+    for (int cb = w0; cb < w1; cb += kScanBatch) {
+      uint4 kv[kScanBatch][2];
+      float ksc[kScanBatch];
+      bool ok[kScanBatch];
 #pragma unroll
-    for (int i = 0; i < kScanBatch; ++i)
-      page[i] = (cb + i < w1) ? (pts_lds ? sh.pts[((cb + i) >> 2) - pg0] : pt_row[(cb + i) >> 2]) : -1;
-#pragma unroll
-    for (int i = 0; i < kScanBatch; ++i) {
-      const int c = cb + i;
-      ok[i] = c < w1 && page[i] >= 0 && (long)page[i] < S.num_pages;
-      kv[i][0] = kv[i][1] = make_uint4(0, 0, 0, 0);
-      ksc[i] = 0.f;
-      if (ok[i]) {
-        const uint8_t* base = S.pages + (long)page[i] * DSA_INDEX_PAGE_BYTES;
-        const uint4* kp = reinterpret_cast<const uint4*>(
-            base + (c & 3) * (kChunkKeys * DSA_INDEX_DIM) + kr * DSA_INDEX_DIM + kc * 32);
-        kv[i][0] = kp[0];
-        kv[i][1] = kp[1];
-        ksc[i] = reinterpret_cast<const float*>(base + DSA_PAGE_TOKENS * DSA_INDEX_DIM)[(c & 3) * kChunkKeys + kr];
+      for (int i = 0; i < kScanBatch; ++i) {
+        const int c = min(cb + i, w1 - 1);
+        const int pg = __builtin_amdgcn_readfirstlane(kPtLds ? sh.pts[(c >> 2) - pg0] : pt_row[c >> 2]);
+        ok[i] = cb + i < w1 && pg >= 0 && (long)pg < S.num_pages;
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t*>(S.pages) + (ok[i] ? (long)pg * DSA_INDEX_PAGE_BYTES : 0L), (short)0,
+            ok[i] ? DSA_INDEX_PAGE_BYTES : 0, 0x00020000);
+        const int off = (c & 3) * (kChunkKeys * DSA_INDEX_DIM) + kr * DSA_INDEX_DIM + kc * 32;
+        kv[i][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+        kv[i][1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off + 16, 0, 0));
+        ksc[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+            r, DSA_PAGE_TOKENS * DSA_INDEX_DIM + ((c & 3) * kChunkKeys + kr) * 4, 0, 0));
       }
-    }
 #pragma unroll
-    for (int i = 0; i < kScanBatch; ++i) {
-      const int c = cb + i;
-      if (c >= w1) break;
-      float acc = 0.f;
-      if (ok[i]) {
+      for (int i = 0; i < kScanBatch; ++i) {
+        const int c = cb + i;
+        if (c >= w1) break;  // uniform
         const v8i kb = v8i{(int)kv[i][0].x, (int)kv[i][0].y, (int)kv[i][0].z, (int)kv[i][0].w,
                            (int)kv[i][1].x, (int)kv[i][1].y, (int)kv[i][1].z, (int)kv[i][1].w};
+        float acc = 0.f;  // an invalid chunk's zero keys give 0
 #pragma unroll
         for (int hg = 0; hg < NHG; ++hg) {
           const v4f d = qk_fp8<VARIANT>(qa[hg], kb);
@@ -1271,26 +1276,30 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
                                                                 false, false)[1]);
         acc += __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(acc), __float_as_uint(acc),
                                                                 false, false)[1]);
-      }
-      const int g = c * kChunkKeys + kr;
-      if (lane < 16 && g < S.slab_stride) {
-        const float v = (ok[i] && g < len) ? acc * ksc[i] : -INFINITY;
-        // device-scope stores when the row's last workgroup reads them back
-        if (S.next_idx) store_dev(&srow[g], v);
-        else srow[g] = v;
-        if (with_hist && g < len) {
-          const uint32_t key = rank_key(v);
-          atomicAdd(&sh.hist[key >> 20], 1u);
-          if (SELECT && S.coop) {
-            reinterpret_cast<CoopShared*>(smem)->keys[g - c0 * kChunkKeys] = key;
-            atomicAdd(&sh.hist[kCoarseOff + (key >> 26)], 1u);
-            kmax = max(kmax, key);
-            nfin += key_is_finite(key) ? 1u : 0u;
+        const int g = c * kChunkKeys + kr;
+        if (lane < 16 && g < S.slab_stride) {
+          const float v = (ok[i] && g < len) ? acc * ksc[i] : -INFINITY;
+          // device-scope stores when the row's last workgroup reads them back
+          if (S.next_idx) store_dev(&srow[g], v);
+          else srow[g] = v;
+          if (with_hist && g < len) {
+            const uint32_t key = rank_key(v);
+            atomicAdd(&sh.hist[key >> 20], 1u);
+            if (SELECT && S.coop) {
+              reinterpret_cast<CoopShared*>(smem)->keys[g - c0 * kChunkKeys] = key;
+              atomicAdd(&sh.hist[kCoarseOff + (key >> 26)], 1u);
+              kmax = max(kmax, key);
+              nfin += key_is_finite(key) ? 1u : 0u;
+            }
           }
         }
       }
     }
-  }
+  };
+  if (pts_lds)
+    run_chunks(std::true_type{});
+  else
+    run_chunks(std::false_type{});
   dbg_stamp(dbk, 2);
   dbg_stamp_wave(dbk, 5, kMainWaves - 1);
   if (!with_hist) return;
@@ -1440,6 +1449,9 @@ int scan_blocks_per_row(int B, int pt_stride, int slab_stride, int att_blocks, b
   if (g_scan_blocks_cap > 0) target = std::min<long>(target, g_scan_blocks_cap);
   long per_row = (target + B - 1) / B;
   per_row = std::min(per_row, std::max(1L, cap_chunks / kMainWaves));
+  // each workgroup's page-table entries must fit the LDS table
+  const long cap_pages = (cap + DSA_PAGE_TOKENS - 1) / DSA_PAGE_TOKENS;
+  per_row = std::max(per_row, (cap_pages + kScanMaxPages - 3) / (kScanMaxPages - 2));
   return (int)std::max(1L, per_row);
 }
 

@@ -297,8 +297,13 @@ __device__ __forceinline__ void dbg_stamp_wave(int blk, int ph, int w) {
   if (threadIdx.x == (unsigned)(w * kWave) && blk < kDbgBlocks)
     g_dbg[blk * kDbgPhases + ph] = __builtin_amdgcn_s_memrealtime();
 }
+// a value instead of a time (the probe reads it from the same table)
+__device__ __forceinline__ void dbg_value(int blk, int ph, unsigned long long v) {
+  if (threadIdx.x == 0 && blk < kDbgBlocks) g_dbg[blk * kDbgPhases + ph] = v;
+}
 #else
 constexpr bool kPhaseStamps = false;
+__device__ __forceinline__ void dbg_value(int, int, unsigned long long) {}
 __device__ __forceinline__ void dbg_stamp(int, int) {}
 __device__ __forceinline__ void dbg_stamp_wave(int, int, int) {}
 #endif
