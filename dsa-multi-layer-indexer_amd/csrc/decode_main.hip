@@ -414,20 +414,15 @@ struct ScanShared {
 
 // Cooperative select: the scan workgroup keeps the rank keys of its own
 // positions and takes part in the row's selection.
-constexpr int kCoopKeys = 8192;      // positions per workgroup
+constexpr int kCoopKeys = 16384;     // positions per workgroup
 constexpr int kCoopMaxBlocks = 256;  // workgroups per row
 constexpr int kPubHdr = 4;           // list header: count, bound key, finite count, max key
 constexpr int kCoopCand = 1024;      // threshold-bin candidates resolved by rank counting
 struct CoopShared {
   ScanShared scan;
   uint32_t keys[kCoopKeys];
-  union {
-    struct {
-      uint32_t cand_key[kCandCap];
-      int cand_idx[kCandCap];
-    };
-    uint32_t pub[kPubWords];  // every workgroup's published list, stride pub_stride()
-  };
+  uint32_t cand_key[kCandCap];  // the histogram form's threshold-bin candidates
+  int cand_idx[kCandCap];
   uint32_t gts[kCoopMaxBlocks];
   uint32_t wave_tmp[4 * kMainWaves];
   uint32_t res[4];
@@ -439,6 +434,8 @@ struct CoopShared {
   uint32_t hred[2 * kMainWaves];   // per wave: list-header reductions
   uint32_t pred[2 * kMainWaves];   // per wave: union counts of pass 2
 };
+
+static_assert(sizeof(CoopShared) <= 160 * 1024, "the cooperative select's LDS must fit one CU");
 
 // Keys a workgroup's list aims to hold: twice its expected share of the K
 // selected keys plus 8.  The list's capacity (a multiple of 4, within the
@@ -1144,7 +1141,7 @@ __device__ __forceinline__ v4f qk_fp8(const v8i& qa, const v8i& kb) {
 }
 
 template <int NHG, int VARIANT, bool SELECT>
-__device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, unsigned char* smem) {
+__device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, int nb, unsigned char* smem) {
   constexpr int kHeads = NHG * 16;
   ScanShared& sh = *reinterpret_cast<ScanShared*>(smem);
   const int t = threadIdx.x;
@@ -1152,7 +1149,6 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   const int dbk = blockIdx.x;
   dbg_stamp(dbk, 0);
   const int cap = min(S.slab_stride, S.pt_stride * DSA_PAGE_TOKENS);
-  const int nb = S.blocks_per_row;
   const int* pt_row = S.page_table + (long)row * S.pt_stride;
   // The page-table entries of this workgroup's chunks are prefetched with the
   // query, speculating that the row is full (len == cap, the usual decode
@@ -1360,6 +1356,45 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
 // launch keeps several workgroups per CU resident).
 constexpr int kRoleAttn = 1, kRoleScan = 2, kRoleSelect = 4;
 
+// Workgroups per row by length (ragged batches of <= 64 rows): every row
+// gets the workgroups its keys and page entries need (the cooperative
+// select holds <= kCoopKeys keys per workgroup, the LDS page table <=
+// kScanMaxPages - 2 pages), and the rest of the launch's nscan workgroups in
+// proportion to its length, so that every workgroup streams about the same
+// number of keys; a row's workgroups stay contiguous in block index.  Each
+// wave computes the same plan from seq_lens (lane r: row r), no barrier.
+// Only max(S.target, what the rows need) workgroups are planned; returns
+// (row, index within the row, the row's workgroups), row -1 for a workgroup
+// no row needs (it exits at once).
+__device__ __forceinline__ int3 plan_row(const ScanArgs& S, int bid, int nscan) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const bool in = lane < S.rows;
+  const long cap = min((long)S.slab_stride, (long)S.pt_stride * DSA_PAGE_TOKENS);
+  const uint32_t len = in ? (uint32_t)max(0L, min((long)S.seq_lens[lane], cap)) : 0u;
+  uint32_t need = 0;
+  if (in) {
+    const uint32_t pages = (len + DSA_PAGE_TOKENS - 1) / DSA_PAGE_TOKENS;
+    need = max(1u, (pages + kScanMaxPages - 3) / (kScanMaxPages - 2));
+    if (S.coop) need = max(need, (len + kCoopKeys - 1) / kCoopKeys);
+  }
+  const uint32_t total = wave_reduce<0>(len);
+  // the workgroups to use: the launcher's target (one per free CU when the
+  // select pins a workgroup to its CU), at least what the rows need
+  const int needed = (int)wave_reduce<0>(need);
+  const uint32_t spare = (uint32_t)max(0, min(nscan, max(S.target, needed)) - needed);
+  uint32_t extra = 0;
+  if (in) extra = total ? (uint32_t)(((uint64_t)spare * len) / total) : spare / (uint32_t)S.rows;
+  const uint32_t rem = spare - wave_reduce<0>(extra);  // < rows
+  extra += (in && (uint32_t)lane < rem) ? 1u : 0u;
+  const uint32_t n = in ? min(need + extra, (uint32_t)S.max_nb) : 0u;
+  const uint32_t incl = wave_scan_incl<0>(n);
+  const uint64_t m = __ballot(in && incl > (uint32_t)bid);
+  if (!m) return make_int3(-1, 0, 0);
+  const int r = __builtin_ctzll(m);
+  const int excl = __builtin_amdgcn_readlane((int)(incl - n), r);
+  return make_int3(r, bid - excl, __builtin_amdgcn_readlane((int)n, r));
+}
+
 template <int NHG, int VARIANT, int ROLES>
 __global__ __launch_bounds__(kMainThreads, ROLES == kRoleScan ? 4 : 1) void decode_main_kernel(AttnArgs A, int n_att,
                                                                                              ScanArgs S) {
@@ -1377,8 +1412,16 @@ __global__ __launch_bounds__(kMainThreads, ROLES == kRoleScan ? 4 : 1) void deco
   }
   if constexpr ((ROLES & kRoleScan) != 0) {
     bid -= n_att;
-    const int row = bid / S.blocks_per_row;
-    scan_block<NHG, VARIANT, (ROLES & kRoleSelect) != 0>(S, row, bid % S.blocks_per_row, smem);
+    int row = bid / S.blocks_per_row, nb = S.blocks_per_row;
+    bid -= row * nb;
+    if (S.balance) {
+      const int3 slot = plan_row(S, blockIdx.x - n_att, (int)gridDim.x - n_att);
+      if (slot.x < 0) return;  // a spare workgroup: no row needs it
+      row = slot.x;
+      bid = slot.y;
+      nb = slot.z;
+    }
+    scan_block<NHG, VARIANT, (ROLES & kRoleSelect) != 0>(S, row, bid, nb, smem);
   }
 }
 
@@ -1517,6 +1560,14 @@ hipError_t launch_decode_main(const AttnArgs* A, int B_att, const ScanArgs* S, i
       }
     }
     n_scan = B_scan * sc.blocks_per_row;
+    // ragged batches: workgroups per row by length (the grid stays B x nb)
+    sc.rows = B_scan;
+    sc.balance = B_scan > 1 && B_scan <= kWave;
+    sc.max_nb = sc.coop ? (int)std::min<long>(kCoopMaxBlocks, device_cus() - 8) : n_scan;
+    // one round of workgroups: when the launch's LDS pins one workgroup per
+    // CU, the CUs the attention leaves (spare workgroups exit at once)
+    const bool big_lds = n_att > 0 || select;
+    sc.target = big_lds ? std::max(device_cus() - n_att, device_cus() / 2) : n_scan;
   }
   if (n_att + n_scan == 0) return hipSuccess;
   size_t lds = sizeof(ScanShared);

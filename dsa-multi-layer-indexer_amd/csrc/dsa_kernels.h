@@ -39,6 +39,10 @@ struct ScanArgs {
   int blocks_per_row;    // filled by the launcher
   int coop;              // filled by the launcher: the row's scan workgroups
                          // select together (group barriers)
+  int rows;              // filled by the launcher: B
+  int balance;           // filled by the launcher: workgroups per row by length
+  int max_nb;            // filled by the launcher: cap on one row's workgroups
+  int target;            // filled by the launcher: workgroups to plan for
 };
 
 // One grid with n attention blocks (A != nullptr, rows B_att) and scan blocks
