@@ -623,9 +623,9 @@ __device__ __forceinline__ void coop_select_hist(CoopShared& cs, unsigned char* 
             (bin > T1 || (bin == T1 && (k > tstar || (tie && run_tie + tie_pre < need3))));
     }
     const uint32_t sel_pre = block_flag_scan(sel, cs.wave_tmp, &sel_tot);
-    if (sel) {
+    if (sel) {  // the slot is < K by construction; clamped anyway
       const int p = p_lo + i;
-      o[base + run_sel + sel_pre] = pt_row[p >> 6] * DSA_PAGE_TOKENS + (p & (DSA_PAGE_TOKENS - 1));
+      o[min(base + run_sel + sel_pre, (uint32_t)K - 1u)] = pt_row[p >> 6] * DSA_PAGE_TOKENS + (p & (DSA_PAGE_TOKENS - 1));
     }
     run_sel += sel_tot;
     run_tie += tie_tot;
@@ -780,7 +780,7 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
           uint32_t b = 0;
           if (lane == 0) b = atomicAdd(&cs.misc[0], (uint32_t)__popcll(m));
           b = (uint32_t)__builtin_amdgcn_readlane((int)b, 0);
-          if (in) cs.ck[b + lane_rank(m)] = k;
+          if (in) cs.ck[min(b + lane_rank(m), (uint32_t)kCoopCand - 1u)] = k;  // < kCoopCand by construction
         }
       }
       __syncthreads();
@@ -817,7 +817,7 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
           uint32_t b = 0;
           if (lane == 0) b = atomicAdd(&cs.misc[2], (uint32_t)__popcll(m));
           b = (uint32_t)__builtin_amdgcn_readlane((int)b, 0);
-          if (pub) store_dev(&mine[b + lane_rank(m)], k);
+          if (pub) store_dev(&mine[min(b + lane_rank(m), (uint32_t)P - 1u)], k);  // < cnt <= P by construction
         }
       }
     }
@@ -1114,7 +1114,7 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
       if (key_is_finite(k) && (all || k > tstar || (tie && tr < need3))) {
         const int p = p_lo + i;
         const int page = pts_lds ? pts[(p >> 6) - pg0] : pt_row[p >> 6];
-        o[pos++] = page * DSA_PAGE_TOKENS + (p & (DSA_PAGE_TOKENS - 1));
+        o[min(pos++, (uint32_t)K - 1u)] = page * DSA_PAGE_TOKENS + (p & (DSA_PAGE_TOKENS - 1));  // < K by construction
       }
       tr += tie ? 1u : 0u;
     }
@@ -1354,7 +1354,9 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
 // workgroups also select.  Each role set is its own instantiation, so a
 // launch pays only for the registers of the roles it runs (a scan-only
 // launch keeps several workgroups per CU resident).
-constexpr int kRoleAttn = 1, kRoleScan = 2, kRoleSelect = 4;
+// kRolePlan: scan workgroups per row by length (ragged batches), a separate
+// instantiation so that batch-1 launches carry none of its code
+constexpr int kRoleAttn = 1, kRoleScan = 2, kRoleSelect = 4, kRolePlan = 8;
 
 // Workgroups per row by length (ragged batches of <= 64 rows): every row
 // gets the workgroups its keys and page entries need (the cooperative
@@ -1396,7 +1398,7 @@ __device__ __forceinline__ int3 plan_row(const ScanArgs& S, int bid, int nscan) 
 }
 
 template <int NHG, int VARIANT, int ROLES>
-__global__ __launch_bounds__(kMainThreads, ROLES == kRoleScan ? 4 : 1) void decode_main_kernel(AttnArgs A, int n_att,
+__global__ __launch_bounds__(kMainThreads, (ROLES & ~kRolePlan) == kRoleScan ? 4 : 1) void decode_main_kernel(AttnArgs A, int n_att,
                                                                                              ScanArgs S) {
   extern __shared__ __align__(16) unsigned char smem[];
   int bid = blockIdx.x;
@@ -1414,7 +1416,7 @@ __global__ __launch_bounds__(kMainThreads, ROLES == kRoleScan ? 4 : 1) void deco
     bid -= n_att;
     int row = bid / S.blocks_per_row, nb = S.blocks_per_row;
     bid -= row * nb;
-    if (S.balance) {
+    if constexpr ((ROLES & kRolePlan) != 0) {
       const int3 slot = plan_row(S, blockIdx.x - n_att, (int)gridDim.x - n_att);
       if (slot.x < 0) return;  // a spare workgroup: no row needs it
       row = slot.x;
@@ -1512,16 +1514,24 @@ static hipError_t launch_k(dim3 grid, size_t lds, size_t lds_max, hipStream_t s,
   return hipGetLastError();
 }
 
+template <int NHG, int PLAN>
+static hipError_t launch_nhg_p(dim3 grid, size_t lds, size_t lds_max, hipStream_t s, const AttnArgs& A,
+                               int n_att, const ScanArgs& S) {
+  const bool att = n_att > 0;
+  if (!att && !S.next_idx)  // plain scan: the only role with the alternative MFMA form
+    return g_scan_variant == 0 ? launch_k<NHG, 0, kRoleScan | PLAN>(grid, lds, lds_max, s, A, n_att, S)
+                               : launch_k<NHG, 1, kRoleScan | PLAN>(grid, lds, lds_max, s, A, n_att, S);
+  if (!att) return launch_k<NHG, 0, kRoleScan | kRoleSelect | PLAN>(grid, lds, lds_max, s, A, n_att, S);
+  return launch_k<NHG, 0, kRoleAttn | kRoleScan | kRoleSelect | PLAN>(grid, lds, lds_max, s, A, n_att, S);
+}
+
 template <int NHG>
 static hipError_t launch_nhg(dim3 grid, size_t lds, size_t lds_max, hipStream_t s, const AttnArgs& A,
                              int n_att, const ScanArgs& S) {
-  const bool att = n_att > 0, scan = S.blocks_per_row > 0 && grid.x > (unsigned)n_att;
+  const bool scan = S.blocks_per_row > 0 && grid.x > (unsigned)n_att;
   if (!scan) return launch_k<4, 0, kRoleAttn>(grid, lds, lds_max, s, A, n_att, S);
-  if (!att && !S.next_idx)  // plain scan: the only role with the alternative MFMA form
-    return g_scan_variant == 0 ? launch_k<NHG, 0, kRoleScan>(grid, lds, lds_max, s, A, n_att, S)
-                               : launch_k<NHG, 1, kRoleScan>(grid, lds, lds_max, s, A, n_att, S);
-  if (!att) return launch_k<NHG, 0, kRoleScan | kRoleSelect>(grid, lds, lds_max, s, A, n_att, S);
-  return launch_k<NHG, 0, kRoleAttn | kRoleScan | kRoleSelect>(grid, lds, lds_max, s, A, n_att, S);
+  return S.balance ? launch_nhg_p<NHG, kRolePlan>(grid, lds, lds_max, s, A, n_att, S)
+                   : launch_nhg_p<NHG, 0>(grid, lds, lds_max, s, A, n_att, S);
 }
 
 hipError_t launch_decode_main(const AttnArgs* A, int B_att, const ScanArgs* S, int B_scan,

@@ -573,7 +573,7 @@ __device__ __forceinline__ void finalize_row(FinShared& sh, const float* __restr
         const int b = __ffs(word) - 1;
         word &= word - 1;
         const int g = i * 32 + b;
-        o[pos++] = map_slots ? (sh.pt[g >> 6] * DSA_PAGE_TOKENS + (g & 63)) : g;
+        o[min(pos++, (uint32_t)K - 1u)] = map_slots ? (sh.pt[g >> 6] * DSA_PAGE_TOKENS + (g & 63)) : g;  // < K by construction
       }
     }
     for (int j = (int)nsel + t; j < K; j += nthr) o[j] = pad;
