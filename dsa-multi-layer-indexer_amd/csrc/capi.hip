@@ -160,6 +160,11 @@ dsa::ScanArgs scan_args(const void* q_fp8, const float* w, const void* index_k, 
   return S;
 }
 
+// Rows from which a layer's indexer runs as two launches (scan, then select
+// beside the attention) instead of one: the fused launch pins one workgroup
+// per CU for the whole scan, which large batches cannot afford.
+constexpr int kSplitLaunchRows = 8;
+
 // One layer on one stream.  attend: the selection its attention reads
 // (nullptr: no attention); with_indexer: scan + select into next_idx, both
 // in the decode launch (the row's last scan workgroup selects).  When the
@@ -180,9 +185,20 @@ int enqueue_layer(const dsa_layer_args* a, const int32_t* attend, bool with_inde
                   a->scores, a->Hidx, a->pt_stride, a->slab_stride, a->topk_scratch, a->next_idx,
                   a->topk);
   const bool own = attention && with_indexer && attend == a->next_idx;
-  int rc = hip_status(dsa::launch_decode_main(attention && !own ? &A : nullptr, a->B,
-                                              with_indexer ? &S : nullptr, a->B, s),
-                      "decode main launch");
+  int rc;
+  if (with_indexer && a->B >= kSplitLaunchRows) {
+    // large batches: a plain scan launch (two workgroups per CU) writes the
+    // scores, then the select loads them beside the attention
+    dsa::ScanArgs P = S;
+    P.next_idx = nullptr;
+    P.hist = nullptr;
+    rc = hip_status(dsa::launch_decode_main(nullptr, 0, &P, a->B, s), "indexer scan launch");
+    if (rc) return rc;
+    S.from_scores = 1;
+  }
+  rc = hip_status(dsa::launch_decode_main(attention && !own ? &A : nullptr, a->B, with_indexer ? &S : nullptr,
+                                          a->B, s),
+                  "decode main launch");
   if (rc) return rc;
   if (own) rc = hip_status(dsa::launch_decode_main(&A, a->B, nullptr, 0, s), "attention launch");
   return rc;

@@ -421,8 +421,13 @@ constexpr int kCoopCand = 1024;      // threshold-bin candidates resolved by ran
 struct CoopShared {
   ScanShared scan;
   uint32_t keys[kCoopKeys];
-  uint32_t cand_key[kCandCap];  // the histogram form's threshold-bin candidates
-  int cand_idx[kCandCap];
+  union {
+    struct {
+      uint32_t cand_key[kCandCap];  // the histogram form's threshold-bin candidates
+      int cand_idx[kCandCap];
+    };
+    uint16_t lpos[kPubWords];  // the list form's published entries: own position index
+  };
   uint32_t gts[kCoopMaxBlocks];
   uint32_t wave_tmp[4 * kMainWaves];
   uint32_t res[4];
@@ -436,6 +441,7 @@ struct CoopShared {
 };
 
 static_assert(sizeof(CoopShared) <= 160 * 1024, "the cooperative select's LDS must fit one CU");
+static_assert(kCoopKeys <= 65536, "own positions are stored as 16-bit indices");
 
 // Keys a workgroup's list aims to hold: twice its expected share of the K
 // selected keys plus 8.  The list's capacity (a multiple of 4, within the
@@ -725,7 +731,7 @@ __device__ __forceinline__ uint32_t lane_rank(uint64_t m) {
 // before this one; each workgroup then writes its own selected positions
 // (KV slots) in position order.
 // Expects, from the scan: the own keys in cs.keys (position order), their
-// fine and coarse histograms, cs.wstat, and cs.misc[2] == 0.
+// fine and coarse histograms, and cs.wstat.
 // pts: this workgroup's page-table entries from page pg0 on (in LDS) when
 // pts_lds, else the row's page table is read from memory.
 __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem, const ScanArgs& S, int bid,
@@ -803,21 +809,27 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
     }
   }
 
-  // ---- publish: keys straight to the list (slots from one LDS atomic per
-  // wave step; the order inside a list does not matter), zero padding, header
+  // ---- publish in position order: thread t takes contiguous positions and
+  // one block scan gives it its slots; the entries' positions stay in LDS
+  // (lpos, shared with the histogram form's candidates, which that form
+  // writes only after this one gave up) for the emit, then zero padding,
+  // header
+  uint16_t* lpos = cs.lpos;  // a list holds <= kPubWords entries
   {
     uint32_t* mine = gpub + (long)bid * P;
     if (!all && lo_b != kNoKeys) {
-      for (int i0 = 0; i0 < nown; i0 += kMainThreads) {
-        const int i = i0 + t;
-        const uint32_t k = i < nown ? cs.keys[i] : 0u;
-        const bool pub = i < nown && k >= lo_b;
-        const uint64_t m = __ballot(pub);
-        if (m) {
-          uint32_t b = 0;
-          if (lane == 0) b = atomicAdd(&cs.misc[2], (uint32_t)__popcll(m));
-          b = (uint32_t)__builtin_amdgcn_readlane((int)b, 0);
-          if (pub) store_dev(&mine[min(b + lane_rank(m), (uint32_t)P - 1u)], k);  // < cnt <= P by construction
+      const int per = (nown + kMainThreads - 1) / kMainThreads;
+      const int i0 = min(nown, t * per), i1 = min(nown, i0 + per);
+      uint32_t c = 0;
+      for (int i = i0; i < i1; ++i) c += cs.keys[i] >= lo_b ? 1u : 0u;
+      uint32_t tot;
+      uint32_t off = block_exclusive_scan(c, cs.wave_tmp, &tot);  // tot == cnt
+      for (int i = i0; i < i1; ++i) {
+        const uint32_t k = cs.keys[i];
+        if (k >= lo_b) {
+          const uint32_t slot = min(off++, (uint32_t)P - 1u);  // < cnt <= P by construction
+          lpos[slot] = (uint16_t)i;
+          store_dev(&mine[slot], k);
         }
       }
     }
@@ -1076,29 +1088,33 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
   const uint32_t nsel = sel_above + (tfin ? need3 : 0u);
   dbg_stamp(dbk, 14);
 
-  // ---- emit own selections in position order: thread t owns the
-  // contiguous positions [t*per, (t+1)*per) of this workgroup ----
-  const int per = (nown + kMainThreads - 1) / kMainThreads;
-  const int i0 = min(nown, t * per), i1 = min(nown, i0 + per);
+  // ---- emit own selections in position order.  Every selected key is in
+  // this workgroup's list (it is >= t* >= every list bound), which holds the
+  // entries in position order: thread t takes contiguous entries.  A row of
+  // <= K tokens publishes nothing and takes every finite key instead. ----
+  const int n_e = all ? nown : (int)cnt;
+  const int per = (n_e + kMainThreads - 1) / kMainThreads;
+  const int e0 = min(n_e, t * per), e1 = min(n_e, e0 + per);
+  const auto entry = [&](int e) { return all ? e : (int)lpos[e]; };  // -> own position index
   uint32_t tie_rank = ties_before;  // rank among all ties of this thread's first tie
   bool any_tie = own_ties > 0;
   if (own_ties < 0) {
     bool has_tie = false;
     if (tfin)
-      for (int i = i0; i < i1; ++i) has_tie |= cs.keys[i] == tstar;
+      for (int e = e0; e < e1; ++e) has_tie |= cs.keys[entry(e)] == tstar;
     any_tie = __syncthreads_or(has_tie);
   }
   if (tfin && any_tie) {
     uint32_t nt = 0;
-    for (int i = i0; i < i1; ++i) nt += (cs.keys[i] == tstar) ? 1u : 0u;
+    for (int e = e0; e < e1; ++e) nt += (cs.keys[entry(e)] == tstar) ? 1u : 0u;
     uint32_t tot;
     tie_rank += block_exclusive_scan(nt, cs.wave_tmp, &tot);
   }
   uint32_t nmine = 0;
   {
     uint32_t tr = tie_rank;
-    for (int i = i0; i < i1; ++i) {
-      const uint32_t k = cs.keys[i];
+    for (int e = e0; e < e1; ++e) {
+      const uint32_t k = cs.keys[entry(e)];
       const bool tie = tfin && k == tstar;
       nmine += (key_is_finite(k) && (all || k > tstar || (tie && tr < need3))) ? 1u : 0u;
       tr += tie ? 1u : 0u;
@@ -1108,7 +1124,8 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
   uint32_t pos = base + block_exclusive_scan(nmine, cs.wave_tmp, &tot_sel);
   {
     uint32_t tr = tie_rank;
-    for (int i = i0; i < i1; ++i) {
+    for (int e = e0; e < e1; ++e) {
+      const int i = entry(e);
       const uint32_t k = cs.keys[i];
       const bool tie = tfin && k == tstar;
       if (key_is_finite(k) && (all || k > tstar || (tie && tr < need3))) {
@@ -1140,7 +1157,10 @@ __device__ __forceinline__ v4f qk_fp8(const v8i& qa, const v8i& kb) {
   return acc;
 }
 
-template <int NHG, int VARIANT, bool SELECT>
+// FROM_SCORES: the row's scores are already in the slab (a plain scan
+// launch wrote them); the workgroup loads its positions' scores instead of
+// scoring the keys, then selects as usual.
+template <int NHG, int VARIANT, bool SELECT, bool FROM_SCORES = false>
 __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, int nb, unsigned char* smem) {
   constexpr int kHeads = NHG * 16;
   ScanShared& sh = *reinterpret_cast<ScanShared*>(smem);
@@ -1157,11 +1177,11 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   const int sc0 = (int)((long)ncap * bid / nb), sc1 = (int)((long)ncap * (bid + 1) / nb);
   const int spg0 = sc0 >> 2;
   const int snpg = (sc1 > sc0) ? ((sc1 - 1) >> 2) - spg0 + 1 : 0;
-  constexpr int kQ = kHeads * DSA_INDEX_DIM / 16;  // uint4 of the query block
+  constexpr int kQ = FROM_SCORES ? 0 : kHeads * DSA_INDEX_DIM / 16;  // uint4 of the query block
   const uint4* qsrc = reinterpret_cast<const uint4*>(S.q8 + (long)row * kHeads * DSA_INDEX_DIM);
   uint4 qv = make_uint4(0, 0, 0, 0);
   if (t < kQ) qv = qsrc[t];
-  const float wv0 = (t < kHeads) ? S.w[(long)row * kHeads + t] : 0.f;
+  const float wv0 = (!FROM_SCORES && t < kHeads) ? S.w[(long)row * kHeads + t] : 0.f;
   const int spv = (snpg <= kMainThreads && t < snpg) ? pt_row[spg0 + t] : 0;
   const int len = max(0, min(S.seq_lens[row], cap));
   const int nchunks = (len + kChunkKeys - 1) / kChunkKeys;
@@ -1174,7 +1194,7 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
     const bool spec_ok = nchunks == ncap && snpg <= kMainThreads;  // then pg0, npg == spg0, snpg
     if (t < kQ) reinterpret_cast<uint4*>(sh.qs)[t] = qv;
     for (int i = t + kMainThreads; i < kQ; i += kMainThreads) reinterpret_cast<uint4*>(sh.qs)[i] = qsrc[i];
-    if (t < kHeads) sh.ws[t] = wv0;
+    if (!FROM_SCORES && t < kHeads) sh.ws[t] = wv0;
     if (pts_lds) {
       if (spec_ok) {
         if (t < npg) sh.pts[t] = spv;
@@ -1192,7 +1212,7 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
     sense = group_sense(S.hist + (long)row * S.hist_row_words + row_sync_off(S.slab_stride) + t * kSyncWords,
                         bid);
   float* srow = S.scores + (long)row * S.slab_stride;
-  {  // slab tail past the last scored chunk -> -inf, spread over the row's blocks
+  if constexpr (!FROM_SCORES) {  // slab tail past the last scored chunk -> -inf, over the row's blocks
     const long tail0 = (long)nchunks * kChunkKeys;
     const long tail = (long)S.slab_stride - tail0;
     if (tail > 0) {
@@ -1209,6 +1229,35 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   const int lane = t & (kWave - 1);
   const int wv = wave_id();
   const int kr = lane & 15, kc = lane >> 4;
+  uint32_t kmax = 0, nfin = 0;  // own keys (cooperative select)
+  if constexpr (FROM_SCORES) {
+    // this workgroup's positions [c0*16, min(c1*16, len)), 8 coalesced
+    // loads in flight per thread
+    const int q_lo = c0 * kChunkKeys, q_n = max(0, min(c1 * kChunkKeys, len) - q_lo);
+    const float* src = srow + q_lo;
+    constexpr int kB = 8;
+    for (int i0 = t; i0 < q_n; i0 += kB * kMainThreads) {
+      float v[kB];
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        const int i = i0 + j * kMainThreads;
+        v[j] = i < q_n ? src[i] : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        const int i = i0 + j * kMainThreads;
+        if (i < q_n) {
+          const uint32_t key = rank_key(v[j]);
+          atomicAdd(&sh.hist[key >> 20], 1u);
+          if (SELECT && S.coop) {  // the coarse bins are summed after the loop
+            reinterpret_cast<CoopShared*>(smem)->keys[i] = key;
+            kmax = max(kmax, key);
+            nfin += key_is_finite(key) ? 1u : 0u;
+          }
+        }
+      }
+    }
+  } else {
   v8i qa[NHG];
   float wr[NHG][4];
 #pragma unroll
@@ -1220,7 +1269,6 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
     for (int r = 0; r < 4; ++r) wr[hg][r] = sh.ws[hg * 16 + 4 * kc + r];
   }
 
-  uint32_t kmax = 0, nfin = 0;  // own keys (cooperative select)
   const int n = c1 - c0;
   const int w0 = c0 + (int)((long)n * wv / kMainWaves);
   const int w1 = c0 + (int)((long)n * (wv + 1) / kMainWaves);
@@ -1296,6 +1344,7 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
     run_chunks(std::true_type{});
   else
     run_chunks(std::false_type{});
+  }  // !FROM_SCORES
   dbg_stamp(dbk, 2);
   dbg_stamp_wave(dbk, 5, kMainWaves - 1);
   if (!with_hist) return;
@@ -1309,12 +1358,23 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
         cs.wstat[2 * wv] = nfin;
         cs.wstat[2 * wv + 1] = kmax;
       }
-      if (t == 0) cs.misc[2] = 0u;  // the list's slot counter
     }
   } else {
     if (S.coop && t < kNumSync) reinterpret_cast<CoopShared*>(smem)->sense[t] = sense;
   }
   __syncthreads();
+  if constexpr (FROM_SCORES && SELECT) {
+    if (S.coop) {  // coarse bin c = the 64 fine bins [64c, 64c + 64): 8 threads per bin
+      const uint4* f4 = reinterpret_cast<const uint4*>(sh.hist + 8 * t);
+      const uint4 a = f4[0], b = f4[1];
+      uint32_t v = a.x + a.y + a.z + a.w + b.x + b.y + b.z + b.w;
+      v += __shfl_xor(v, 1);
+      v += __shfl_xor(v, 2);
+      v += __shfl_xor(v, 4);
+      if ((t & 7) == 0) sh.hist[kCoarseOff + (t >> 3)] = v;
+      __syncthreads();
+    }
+  }
   dbg_stamp(dbk, 6);
   uint32_t* rs = S.hist + (long)row * S.hist_row_words;
   if (!S.coop)
@@ -1356,7 +1416,8 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
 // launch keeps several workgroups per CU resident).
 // kRolePlan: scan workgroups per row by length (ragged batches), a separate
 // instantiation so that batch-1 launches carry none of its code
-constexpr int kRoleAttn = 1, kRoleScan = 2, kRoleSelect = 4, kRolePlan = 8;
+// kRoleFromScores: the select loads the scores a plain scan launch wrote
+constexpr int kRoleAttn = 1, kRoleScan = 2, kRoleSelect = 4, kRolePlan = 8, kRoleFromScores = 16;
 
 // Workgroups per row by length (ragged batches of <= 64 rows): every row
 // gets the workgroups its keys and page entries need (the cooperative
@@ -1423,7 +1484,7 @@ __global__ __launch_bounds__(kMainThreads, (ROLES & ~kRolePlan) == kRoleScan ? 4
       bid = slot.y;
       nb = slot.z;
     }
-    scan_block<NHG, VARIANT, (ROLES & kRoleSelect) != 0>(S, row, bid, nb, smem);
+    scan_block<NHG, VARIANT, (ROLES & kRoleSelect) != 0, (ROLES & kRoleFromScores) != 0>(S, row, bid, nb, smem);
   }
 }
 
@@ -1518,6 +1579,11 @@ template <int NHG, int PLAN>
 static hipError_t launch_nhg_p(dim3 grid, size_t lds, size_t lds_max, hipStream_t s, const AttnArgs& A,
                                int n_att, const ScanArgs& S) {
   const bool att = n_att > 0;
+  if (S.from_scores) {
+    if (!att) return launch_k<NHG, 0, kRoleScan | kRoleSelect | kRoleFromScores | PLAN>(grid, lds, lds_max, s, A, n_att, S);
+    return launch_k<NHG, 0, kRoleAttn | kRoleScan | kRoleSelect | kRoleFromScores | PLAN>(grid, lds, lds_max, s, A,
+                                                                                         n_att, S);
+  }
   if (!att && !S.next_idx)  // plain scan: the only role with the alternative MFMA form
     return g_scan_variant == 0 ? launch_k<NHG, 0, kRoleScan | PLAN>(grid, lds, lds_max, s, A, n_att, S)
                                : launch_k<NHG, 1, kRoleScan | PLAN>(grid, lds, lds_max, s, A, n_att, S);

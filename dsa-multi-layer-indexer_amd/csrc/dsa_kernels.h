@@ -43,6 +43,7 @@ struct ScanArgs {
   int balance;           // filled by the launcher: workgroups per row by length
   int max_nb;            // filled by the launcher: cap on one row's workgroups
   int target;            // filled by the launcher: workgroups to plan for
+  int from_scores;       // the select reads the slab instead of scoring keys
 };
 
 // One grid with n attention blocks (A != nullptr, rows B_att) and scan blocks

@@ -4,7 +4,9 @@ The layer composite (scan + select in one launch, no attend set) must give
 the oracle's top-k of the scores it produced, mapped to KV slots, bit-exact
 (reference select_topk, attention_core.py:66-91, ties to the lower index).
 Covered: the cooperative select (all scan workgroups of a row; default) and
-the single-workgroup select, on ragged rows, rows of <= topk tokens, rows
+the single-workgroup select, fused into the scan launch (< 8 rows) and as a
+select launch over the scan's scores (>= 8 rows), on ragged rows, rows of
+<= topk tokens, rows
 with many equal scores at the threshold, and rows whose threshold bin
 overflows the candidate list (every score equal).  No group wait may expire.
 """
@@ -55,6 +57,10 @@ CASES = [
     ([2048, 2049, 1], 2, None),
     ([20000, 9000], 3, "dup"),
     ([6000, 4097], 4, "equal"),
+    # >= 8 rows: the indexer runs as a scan launch, then a select launch that
+    # loads the scores; ragged, with rows at or below topk
+    ([40000, 300, 2048, 17000, 1, 9000, 31000, 2049, 12000, 500, 26000, 4000], 5, None),
+    ([9000, 7000, 3000, 12000, 2500, 8000, 6000, 11000, 5000], 6, "dup"),
 ]
 
 

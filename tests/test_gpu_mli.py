@@ -52,7 +52,7 @@ def _serial(layers, first):
         else:
             sels.append(None)
             new_carried = carried
-        outs.append(ops.sparse_mla_decode(L.q_bf16, L.kv_pool, att))
+        outs.append(ops.sparse_mla_decode(L.q_bf16, L.kv_pool, att, nsplit=L.nsplit))
         carried = new_carried
     torch.cuda.synchronize()
     return outs, sels
@@ -171,4 +171,32 @@ def test_mli_lag_depth_and_indexcache_pattern(dev, depth, pattern, cold):
             ref = ops.sparse_mla_decode(L.q_bf16, L.kv_pool, att, nsplit=L.nsplit)
             torch.cuda.synchronize()
             assert _eq(outs[i], ref), f"{mode} layer {i} attends layer {src[i]}"
+    sched.close()
+
+
+def test_mli_large_batch_two_launch_layers_equal_serial(dev):
+    """>= 8 rows: each indexer layer is a scan launch and a select launch
+    (beside the attention); outputs and selections equal the standalone ops."""
+    from lagged_indexer_dsa_amd import synthetic as S
+    from lagged_indexer_dsa_amd.decode import MLISchedule
+
+    print("[mli] 8-row batch", flush=True)
+    lens = [9000, 3000, 2048, 70, 5000, 12000, 800, 4097]
+    pt, num_pages = S.make_page_table(lens, seed=3, device=dev)
+    # a fixed split count: the shared launch would otherwise pick its own
+    # (fewer splits per row at this batch), which rounds differently
+    layers = [S.make_decode_layer(lens, seed=60 + i, device=dev, page_table=pt, num_pages=num_pages, nsplit=8)
+              for i in range(3)]
+    first = S.random_selection(lens, 2048, pt, seed=97, device=dev)
+    ref_out, ref_sel = _serial(layers, first)
+    sched = MLISchedule(layers, first)
+    for mode in ("eager", "graph", "graph"):
+        for L in layers:
+            L.out.zero_(); L.next_idx.fill_(-7)
+        torch.cuda.synchronize()
+        sched.run_eager() if mode == "eager" else sched.replay()
+        outs, sels = _snap(layers)
+        for i in range(len(layers)):
+            assert _eq(outs[i], ref_out[i]), f"{mode} layer {i} output"
+            assert _eq(sels[i], ref_sel[i]), f"{mode} layer {i} selection"
     sched.close()
