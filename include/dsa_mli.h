@@ -142,8 +142,10 @@ int dsa_sparse_mla_decode(const void* q_bf16, const void* kv_pool,
  * (4) One DSA decode layer on one stream:
  *   indexer scan -> top-k (position order, KV-slot output into next_idx),
  *   and attention over attend_idx (the lagged set: the attention and the
- *   scan then share ONE launch), or over this layer's own fresh selection
- *   when attend_idx == NULL (baseline DSA: scan, select, then attention).
+ *   scan then share ONE launch; from B = 8 rows the scan is a launch of its
+ *   own and the select shares the attention's), or over this layer's own
+ *   fresh selection when attend_idx == NULL (baseline DSA: scan, select,
+ *   then attention).
  * scores [B, slab_stride] fp32 scratch; next_idx [B, topk] int32.
  * Replaces: DSALayer.fused_attention_and_indices (dsa_layer.py:173-192)
  * for one decode row per request.
@@ -182,8 +184,9 @@ int dsa_decode_layer(const dsa_layer_args* args, void* stream);
  * Layer i attends the selection of the most recent earlier layer that runs
  * an indexer (its attend_idx when given; layer 0 must be given one), and
  * layer i's indexer scan runs in the SAME launch as layer i's attention
- * (role-decoupled workgroups), followed by layer i's top-k select, which
- * layer i+1 attends.  A layer whose q_fp8 is NULL runs no indexer (IndexCache
+ * (role-decoupled workgroups; from B = 8 rows the scan runs just before it
+ * and the select shares the attention's launch), followed by layer i's
+ * top-k select, which layer i+1 attends.  A layer whose q_fp8 is NULL runs no indexer (IndexCache
  * reuse); one whose q_bf16 is NULL runs no attention.  Everything is on one
  * stream: the overlap of indexer and attention is inside each launch.
  * Replaces: DSAModel.forward LAGGED_FUSED (model.py:109-136) and the serving
