@@ -61,6 +61,13 @@ CASES = [
     # loads the scores; ragged, with rows at or below topk
     ([40000, 300, 2048, 17000, 1, 9000, 31000, 2049, 12000, 500, 26000, 4000], 5, None),
     ([9000, 7000, 3000, 12000, 2500, 8000, 6000, 11000, 5000], 6, "dup"),
+    # zero-length rows (the length plan still gives each row a workgroup)
+    ([0, 5000, 0, 3000], 7, None),
+    # >= 8 rows, all scores equal: the score-loading select's histogram form
+    ([9000] * 8 + [0], 8, "equal"),
+    # 64 rows (the largest batch the length plan covers) and 65 (uniform)
+    ([int(x) for x in np.random.default_rng(9).integers(1, 20000, 64)], 9, None),
+    ([int(x) for x in np.random.default_rng(10).integers(1, 5000, 65)], 10, None),
 ]
 
 
