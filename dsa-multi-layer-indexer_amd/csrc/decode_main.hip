@@ -131,8 +131,35 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
   const int k0 = min(A.topk, sp * kps), k1 = min(A.topk, k0 + kps);
   const int* idx_row = A.idx + (long)b * A.topk;
 
-  // first tile's slot before the query (the gather depends on it)
-  int slot_next = (k0 + 16 * wv + kr < k1) ? idx_row[k0 + 16 * wv + kr] : -1;
+  // the first two tiles' slots before the query (the gathers depend on them)
+  const int slot0 = (k0 + 16 * wv + kr < k1) ? idx_row[k0 + 16 * wv + kr] : -1;
+  int slot_next = (k0 + kTile + 16 * wv + kr < k1) ? idx_row[k0 + kTile + 16 * wv + kr] : -1;
+  // this lane's bytes of one key row (zeros for an invalid slot)
+  struct RowRegs {
+    uint4 nope[8], rope[2];
+    float sc;
+    bool valid;
+  };
+  const auto load_row = [&](int slot, RowRegs& r) {
+    r.valid = slot >= 0 && (long)slot < A.kv_rows;
+    r.sc = 0.f;
+    if (r.valid) {
+      const uint8_t* rowp = A.pool + (long)slot * DSA_LATENT_ROW_BYTES;
+      const uint4* np = reinterpret_cast<const uint4*>(rowp + 128 * kc);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) r.nope[i] = np[i];
+      r.sc = reinterpret_cast<const float*>(rowp + DSA_LATENT_DIM)[kc];
+      const uint4* rp = reinterpret_cast<const uint4*>(rowp + DSA_LATENT_DIM + 16 + 32 * kc);
+      r.rope[0] = rp[0];
+      r.rope[1] = rp[1];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) r.nope[i] = make_uint4(0, 0, 0, 0);
+      r.rope[0] = r.rope[1] = make_uint4(0, 0, 0, 0);
+    }
+  };
+  RowRegs cur;
+  load_row(slot0, cur);
 
   // Q (A operand): step s<16 -> dims 128kc + 8s; s = 16, 17 -> 512 + 16kc + 8(s-16)
   uint4 qa[18];
@@ -151,28 +178,18 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
   for (int nt = 0; nt < 4; ++nt) o[nt] = v4f{0.f, 0.f, 0.f, 0.f};
 
   for (int tile0 = k0; tile0 < k1; tile0 += kTile) {
-    const int slot = slot_next;
-    const bool valid = slot >= 0 && (long)slot < A.kv_rows;
-    const uint8_t* rowp = A.pool + (valid ? (long)slot : 0L) * DSA_LATENT_ROW_BYTES;
-    uint4 nope[8], rope[2];
-    float sc = 0.f;
-    if (valid) {
-      const uint4* np = reinterpret_cast<const uint4*>(rowp + 128 * kc);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) nope[i] = np[i];
-      sc = reinterpret_cast<const float*>(rowp + DSA_LATENT_DIM)[kc];
-      const uint4* rp = reinterpret_cast<const uint4*>(rowp + DSA_LATENT_DIM + 16 + 32 * kc);
-      rope[0] = rp[0];
-      rope[1] = rp[1];
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) nope[i] = make_uint4(0, 0, 0, 0);
-      rope[0] = rope[1] = make_uint4(0, 0, 0, 0);
-    }
-    {
-      const int jn = tile0 + kTile + 16 * wv + kr;  // next tile's slot, early
+    // the next tile's gather is in flight while this tile is computed
+    const bool more = tile0 + kTile < k1;  // uniform
+    RowRegs nxt;
+    if (more) {
+      load_row(slot_next, nxt);
+      const int jn = tile0 + 2 * kTile + 16 * wv + kr;  // the slot after it, early
       slot_next = (jn < k1) ? idx_row[jn] : -1;
     }
+    const bool valid = cur.valid;
+    const uint4* nope = cur.nope;
+    const uint4* rope = cur.rope;
+    const float sc = cur.sc;
 
     // dequantise -> QK MFMA + row-major value tile (16-byte stores)
     const int kl = 16 * wv + kr;
@@ -249,6 +266,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
       }
     }
     __syncthreads();
+    if (more) cur = nxt;
   }
 
   dbg_stamp(dbk, 3);
