@@ -303,6 +303,18 @@ int dsa_topk(const float* scores, const int32_t* seq_lens, const int32_t* page_t
                       topk, flags);
   if (rc) return rc;
   hipStream_t s = (hipStream_t)stream;
+  if (flags == DSA_TOPK_POSITION_ORDER) {
+    // position order: one launch of the decode kernel's select over the given
+    // scores (its workgroups split each row and select together)
+    dsa::ScanArgs S = scan_args(nullptr, nullptr, nullptr, 0, page_table, seq_lens,
+                                const_cast<float*>(scores), 16,
+                                page_table ? pt_stride : (slab_stride + DSA_PAGE_TOKENS - 1) / DSA_PAGE_TOKENS,
+                                slab_stride, scratch, out_idx, topk);
+    S.from_scores = 1;
+    S.standalone = 1;
+    S.pad = pad_value;
+    return hip_status(dsa::launch_decode_main(nullptr, 0, &S, B, s), "top-k launch");
+  }
   rc = hip_status(dsa::launch_topk_hist(scores, seq_lens, scratch, B, slab_stride, topk, s),
                   "top-k histogram launch");
   if (rc) return rc;

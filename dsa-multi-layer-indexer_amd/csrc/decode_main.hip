@@ -488,6 +488,7 @@ __host__ __device__ inline int pub_stride(int nb, int K) {
 // A candidate list that would overflow (more than kCandCap keys in bin T1,
 // e.g. many equal scores) hands the row to the single-workgroup select
 // instead.  The last workgroup to finish re-arms the row's scratch.
+template <bool TOPK>
 __device__ __forceinline__ void coop_select_hist(CoopShared& cs, unsigned char* smem, const ScanArgs& S,
                                                  int bid, int nb, int len, int p_lo, int p_hi, uint32_t* rs,
                                                  const float* srow, const int* pt_row, int* o) {
@@ -527,7 +528,8 @@ __device__ __forceinline__ void coop_select_hist(CoopShared& cs, unsigned char* 
     if (bid != nb - 1) return;
     __syncthreads();
     FinShared& fs = *reinterpret_cast<FinShared*>(smem);
-    finalize_row(fs, srow, len, pt_row, S.pt_stride, rs, o, S.slab_stride, K, 0, -1, /*fused=*/true);
+    finalize_row(fs, srow, len, pt_row, S.pt_stride, rs, o, S.slab_stride, K, 0, TOPK ? S.pad : -1,
+                 /*fused=*/true);
     return;
   }
 
@@ -649,13 +651,14 @@ __device__ __forceinline__ void coop_select_hist(CoopShared& cs, unsigned char* 
     const uint32_t sel_pre = block_flag_scan(sel, cs.wave_tmp, &sel_tot);
     if (sel) {  // the slot is < K by construction; clamped anyway
       const int p = p_lo + i;
-      o[min(base + run_sel + sel_pre, (uint32_t)K - 1u)] = pt_row[p >> 6] * DSA_PAGE_TOKENS + (p & (DSA_PAGE_TOKENS - 1));
+      o[min(base + run_sel + sel_pre, (uint32_t)K - 1u)] =
+          (TOPK && !pt_row) ? p : pt_row[p >> 6] * DSA_PAGE_TOKENS + (p & (DSA_PAGE_TOKENS - 1));
     }
     run_sel += sel_tot;
     run_tie += tie_tot;
   }
   if (bid == nb - 1)
-    for (int j = (int)nsel + t; j < K; j += kMainThreads) o[j] = -1;
+    for (int j = (int)nsel + t; j < K; j += kMainThreads) o[j] = TOPK ? S.pad : -1;
 
   // ---- re-arm: everyone has read the histogram (barrier 2 passed) ----
   for (int i = kNB1 * bid / nb + t; i < kNB1 * (bid + 1) / nb; i += kMainThreads) rs[kHistOff + i] = 0u;
@@ -752,6 +755,7 @@ __device__ __forceinline__ uint32_t lane_rank(uint64_t m) {
 // fine and coarse histograms, and cs.wstat.
 // pts: this workgroup's page-table entries from page pg0 on (in LDS) when
 // pts_lds, else the row's page table is read from memory.
+template <bool TOPK>
 __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem, const ScanArgs& S, int bid,
                                             int nb, int len, int p_lo, int p_hi, uint32_t* rs,
                                             const float* srow, const int* pt_row, int* o, const int* pts,
@@ -954,7 +958,7 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
     dbg_stamp(dbk, 4);
     if (!ok) {
       dbg_stamp(dbk, 13);
-      coop_select_hist(cs, smem, S, bid, nb, len, p_lo, p_hi, rs, srow, pt_row, o);
+      coop_select_hist<TOPK>(cs, smem, S, bid, nb, len, p_lo, p_hi, rs, srow, pt_row, o);
       return;
     }
     // pass 2: finite keys above T1's bin are selected: count them (and
@@ -1148,14 +1152,15 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
       const bool tie = tfin && k == tstar;
       if (key_is_finite(k) && (all || k > tstar || (tie && tr < need3))) {
         const int p = p_lo + i;
-        const int page = pts_lds ? pts[(p >> 6) - pg0] : pt_row[p >> 6];
-        o[min(pos++, (uint32_t)K - 1u)] = page * DSA_PAGE_TOKENS + (p & (DSA_PAGE_TOKENS - 1));  // < K by construction
+        int v = p;  // a position, or its KV slot when there is a page table
+        if (!TOPK || pt_row) v = (pts_lds ? pts[(p >> 6) - pg0] : pt_row[p >> 6]) * DSA_PAGE_TOKENS + (p & (DSA_PAGE_TOKENS - 1));
+        o[min(pos++, (uint32_t)K - 1u)] = v;  // < K by construction
       }
       tr += tie ? 1u : 0u;
     }
   }
   if (bid == nb - 1)
-    for (int j = (int)nsel + t; j < K; j += kMainThreads) o[j] = -1;
+    for (int j = (int)nsel + t; j < K; j += kMainThreads) o[j] = TOPK ? S.pad : -1;
   dbg_stamp(dbk, 11);
 }
 
@@ -1178,7 +1183,7 @@ __device__ __forceinline__ v4f qk_fp8(const v8i& qa, const v8i& kb) {
 // FROM_SCORES: the row's scores are already in the slab (a plain scan
 // launch wrote them); the workgroup loads its positions' scores instead of
 // scoring the keys, then selects as usual.
-template <int NHG, int VARIANT, bool SELECT, bool FROM_SCORES = false>
+template <int NHG, int VARIANT, bool SELECT, bool FROM_SCORES = false, bool TOPK = false>
 __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, int nb, unsigned char* smem) {
   constexpr int kHeads = NHG * 16;
   ScanShared& sh = *reinterpret_cast<ScanShared*>(smem);
@@ -1187,7 +1192,10 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   const int dbk = blockIdx.x;
   dbg_stamp(dbk, 0);
   const int cap = min(S.slab_stride, S.pt_stride * DSA_PAGE_TOKENS);
-  const int* pt_row = S.page_table + (long)row * S.pt_stride;
+  // TOPK (the standalone top-k over given scores): no page table means the
+  // output is positions
+  const int* pt_row = (TOPK && !S.page_table) ? nullptr : S.page_table + (long)row * S.pt_stride;
+  const bool has_pt = !TOPK || pt_row != nullptr;
   // The page-table entries of this workgroup's chunks are prefetched with the
   // query, speculating that the row is full (len == cap, the usual decode
   // case) so the prefetch need not wait for seq_lens; a shorter row reloads.
@@ -1200,14 +1208,14 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   uint4 qv = make_uint4(0, 0, 0, 0);
   if (t < kQ) qv = qsrc[t];
   const float wv0 = (!FROM_SCORES && t < kHeads) ? S.w[(long)row * kHeads + t] : 0.f;
-  const int spv = (snpg <= kMainThreads && t < snpg) ? pt_row[spg0 + t] : 0;
+  const int spv = (has_pt && snpg <= kMainThreads && t < snpg) ? pt_row[spg0 + t] : 0;
   const int len = max(0, min(S.seq_lens[row], cap));
   const int nchunks = (len + kChunkKeys - 1) / kChunkKeys;
   const int c0 = (int)((long)nchunks * bid / nb);
   const int c1 = (int)((long)nchunks * (bid + 1) / nb);
   const int pg0 = c0 >> 2;
   const int npg = (c1 > c0) ? ((c1 - 1) >> 2) - pg0 + 1 : 0;
-  const bool pts_lds = npg <= kScanMaxPages;
+  const bool pts_lds = has_pt && npg <= kScanMaxPages;
   {
     const bool spec_ok = nchunks == ncap && snpg <= kMainThreads;  // then pg0, npg == spg0, snpg
     if (t < kQ) reinterpret_cast<uint4*>(sh.qs)[t] = qv;
@@ -1404,7 +1412,7 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   if constexpr (!SELECT) return;
   if (!S.next_idx) return;
   if (S.coop) {
-    coop_select(*reinterpret_cast<CoopShared*>(smem), smem, S, bid, nb, len, c0 * kChunkKeys,
+    coop_select<TOPK>(*reinterpret_cast<CoopShared*>(smem), smem, S, bid, nb, len, c0 * kChunkKeys,
                 min(c1 * kChunkKeys, len), rs, srow, pt_row, S.next_idx + (long)row * S.topk, sh.pts, pg0,
                 pts_lds);
     return;
@@ -1421,7 +1429,7 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   dbg_stamp(dbk, 4);
   FinShared& fs = *reinterpret_cast<FinShared*>(smem);  // the scan's LDS is dead now
   finalize_row(fs, srow, len, pt_row, S.pt_stride, rs, S.next_idx + (long)row * S.topk,
-               S.slab_stride, S.topk, /*sorted=*/0, /*pad=*/-1, /*fused=*/true);
+               S.slab_stride, S.topk, /*sorted=*/0, TOPK ? S.pad : -1, /*fused=*/true);
   dbg_stamp(dbk, 5);
 }
 
@@ -1435,7 +1443,10 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
 // kRolePlan: scan workgroups per row by length (ragged batches), a separate
 // instantiation so that batch-1 launches carry none of its code
 // kRoleFromScores: the select loads the scores a plain scan launch wrote
-constexpr int kRoleAttn = 1, kRoleScan = 2, kRoleSelect = 4, kRolePlan = 8, kRoleFromScores = 16;
+// kRoleTopk: with kRoleFromScores, the standalone top-k (caller's pad value;
+//   positions when there is no page table)
+constexpr int kRoleAttn = 1, kRoleScan = 2, kRoleSelect = 4, kRolePlan = 8, kRoleFromScores = 16,
+              kRoleTopk = 32;
 
 // Workgroups per row by length (ragged batches of <= 64 rows): every row
 // gets the workgroups its keys and page entries need (the cooperative
@@ -1502,7 +1513,8 @@ __global__ __launch_bounds__(kMainThreads, (ROLES & ~kRolePlan) == kRoleScan ? 4
       bid = slot.y;
       nb = slot.z;
     }
-    scan_block<NHG, VARIANT, (ROLES & kRoleSelect) != 0, (ROLES & kRoleFromScores) != 0>(S, row, bid, nb, smem);
+    scan_block<NHG, VARIANT, (ROLES & kRoleSelect) != 0, (ROLES & kRoleFromScores) != 0, (ROLES & kRoleTopk) != 0>(
+        S, row, bid, nb, smem);
   }
 }
 
@@ -1598,6 +1610,8 @@ static hipError_t launch_nhg_p(dim3 grid, size_t lds, size_t lds_max, hipStream_
                                int n_att, const ScanArgs& S) {
   const bool att = n_att > 0;
   if (S.from_scores) {
+    if (S.standalone) return launch_k<1, 0, kRoleScan | kRoleSelect | kRoleFromScores | kRoleTopk | PLAN>(
+        grid, lds, lds_max, s, A, n_att, S);
     if (!att) return launch_k<NHG, 0, kRoleScan | kRoleSelect | kRoleFromScores | PLAN>(grid, lds, lds_max, s, A, n_att, S);
     return launch_k<NHG, 0, kRoleAttn | kRoleScan | kRoleSelect | kRoleFromScores | PLAN>(grid, lds, lds_max, s, A,
                                                                                          n_att, S);
@@ -1647,7 +1661,7 @@ hipError_t launch_decode_main(const AttnArgs* A, int B_att, const ScanArgs* S, i
       const long min_nb = (cap_chunks + kCoopKeys / kChunkKeys - 1) / (kCoopKeys / kChunkKeys);
       const long max_nb = std::min<long>(kCoopMaxBlocks, device_cus() - 8);
       const long bw = bitmap_words(sc.slab_stride);
-      long nb = std::max<long>(sc.blocks_per_row, min_nb);
+      long nb = std::max<long>(std::min<long>(sc.blocks_per_row, max_nb), min_nb);
       if (nb <= max_nb && nb <= bw) {
         sc.blocks_per_row = (int)nb;
         sc.coop = 1;

@@ -44,6 +44,9 @@ struct ScanArgs {
   int max_nb;            // filled by the launcher: cap on one row's workgroups
   int target;            // filled by the launcher: workgroups to plan for
   int from_scores;       // the select reads the slab instead of scoring keys
+  int standalone;        // with from_scores: the top-k op alone (pad below;
+                         // page_table may be null: positions are emitted)
+  int pad;               // standalone: value of the unused output entries
 };
 
 // One grid with n attention blocks (A != nullptr, rows B_att) and scan blocks

@@ -97,9 +97,15 @@ int dsa_indexer_scan(const void* q_fp8, const float* w, const void* index_k,
  * page_table[b*pt_stride + g/64]*64 + g%64 (position order only).
  *   scores  [B, slab_stride] fp32;  out_idx [B, topk] int32
  *   scratch dsa_topk_scratch_bytes(B, slab_stride) bytes, zero-filled once
- *           before the first call; every call leaves it zeroed again, so
- *           calls chain and graph replays need no memset.  Two calls that
- *           overlap in time must not share a scratch buffer.
+ *           before the first call; every call leaves it ready for the next
+ *           (counters re-armed, barrier flags consistent), so calls chain and
+ *           graph replays need no memset; zeroing it again between calls is
+ *           harmless.  Two calls that overlap in time must not share a
+ *           scratch buffer.
+ * DSA_TOPK_POSITION_ORDER runs as ONE launch: the workgroups of a row each
+ * load a slice of its scores and select together (the decode layer's
+ * cooperative select); DSA_TOPK_SORTED runs as two launches (histogram,
+ * then per-slice filter and a sorting finalize).
  * Requires topk <= 8192 (<= 4096 with DSA_TOPK_SORTED) and
  * slab_stride <= DSA_TOPK_MAX_CTX.
  * Replaces: reference attention_core.py:66-91 (select_topk), and on the GPU

@@ -132,3 +132,47 @@ def test_topk_undersized_buffers_rejected_before_launch(dev):
     with pytest.raises(RuntimeError):
         ops.topk(sc, lens, 2048, out=torch.empty(2, 1024, dtype=torch.int32, device=dev))
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("k", [1, 2047, 8192])
+def test_topk_position_order_large_k_and_lengths_past_slab(dev, k):
+    """Position order runs the cooperative select: k up to its maximum, rows
+    whose seq_len exceeds the slab (clamped) or is negative (empty)."""
+    rng = np.random.default_rng(11 + k)
+    print(f"[topk] position order k={k}", flush=True)
+    s = rng.standard_normal((5, 40000)).astype(np.float32)
+    s[3] = np.round(s[3] * 4) / 4           # ties at the threshold
+    _check(s, [40000, 90000, 8192, 39999, -3], k, False, dev, pad=-5)
+
+
+@pytest.mark.parametrize("B", [64, 65, 300])
+def test_topk_position_order_many_rows(dev, B):
+    """64 rows (per-row workgroup plan), 65 and 300 rows (uniform split)."""
+    rng = np.random.default_rng(B)
+    print(f"[topk] position order B={B}", flush=True)
+    s = rng.standard_normal((B, 6000)).astype(np.float32)
+    lens = rng.integers(0, 6001, B)
+    lens[: B // 4] = 6000
+    pt = rng.integers(0, 100000, (B, 94)).astype(np.int32)
+    _check(s, lens, 2048, False, dev)
+    _check(s, lens, 2048, False, dev, pt=pt)
+
+
+def test_topk_position_and_sorted_share_scratch(dev):
+    """Alternating the two orders over one scratch buffer: each call leaves
+    the scratch ready for the next."""
+    from lagged_indexer_dsa_amd import ops
+
+    rng = np.random.default_rng(21)
+    print("[topk] shared scratch", flush=True)
+    B, slab, k = 3, 50000, 2048
+    lens = np.array([50000, 20000, 1000], dtype=np.int32)
+    scratch = ops.topk_scratch(B, slab, dev)
+    l = torch.from_numpy(lens).to(dev)
+    for it in range(6):
+        sorted_ = it % 2 == 1
+        s = rng.standard_normal((B, slab)).astype(np.float32)
+        out = ops.topk(torch.from_numpy(s).to(dev), l, k, sorted=sorted_, scratch=scratch)
+        torch.cuda.synchronize()
+        ref = O.topk_select(s, lens, k, sorted_=sorted_)
+        assert np.array_equal(out.cpu().numpy(), ref), f"call {it} sorted={sorted_}"
