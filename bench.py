@@ -159,7 +159,18 @@ def main() -> int:
                     help="cap on the rotated layer sets (1: no Infinity-Cache defeat)")
     ap.add_argument("--profile-main", action="store_true",
                     help="only the calibration copy and the timed region (profiler runs)")
+    ap.add_argument("--graph-packet-capture", action="store_true",
+                    help="keep the HIP runtime's default graph launch mode (captured AQL packets), "
+                         "which adds ~3.5 us to every replay")
     args = ap.parse_args()
+    # The HIP runtime replays a graph either from AQL packets it captured at
+    # instantiation (its default) or by launching the graph's nodes on the
+    # stream.  On this stack the first costs ~4.7 us per replay more than
+    # eager launches, the second ~1.2 us; the kernels and their order are the
+    # same.  Read once at runtime start-up, so it is set before torch loads.
+    if not args.graph_packet_capture:
+        os.environ.setdefault("DEBUG_CLR_GRAPH_PACKET_CAPTURE", "0")
+    packet_capture = os.environ.get("DEBUG_CLR_GRAPH_PACKET_CAPTURE", "1") != "0"
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only (one TP-8 share of heads); "
                                    "multi-GPU runs are not part of it", "n_gpus": args.gpus}))
@@ -339,6 +350,7 @@ def main() -> int:
                    "layers_per_step": n_layers, "index_heads": 64, "attn_heads": 16,
                    "topk": 2048, "page_tokens": 64,
                    "schedule": "MLI lag, one fused launch per layer, 1 hipGraph",
+                   "hip_graph_packet_capture": packet_capture,
                    "rotated_sets": n_sets, "bytes_per_step": step_bytes},
         "tokens_per_s": round(B / (us_layer * 1e-6), 1),
         "indexer_scan_GBps": round(scan_gbs, 1),
