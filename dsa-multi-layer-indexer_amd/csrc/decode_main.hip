@@ -795,39 +795,29 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
       lo_b = next_bin_key(th.bin);
       cnt = th.above;
     } else {
-      // the bin's keys, then the smallest of them, v, with #{own >= v} <= P
-      // by rank counting (each wave the same)
-      if (t == 0) cs.misc[0] = 0u;
+      // the bin split by the next 8 key bits: the bound is the lowest
+      // sub-bin edge with #{own >= edge} <= P (each wave the same).  Every
+      // own key >= the edge is listed, as the list requires.
+      uint32_t* sub = cs.ck;  // 256 counters; the candidates come later
+      if (t < 256) sub[t] = 0u;
       __syncthreads();
-      for (int i0 = 0; i0 < nown; i0 += kMainThreads) {
-        const int i = i0 + t;
-        const uint32_t k = i < nown ? cs.keys[i] : 0u;
-        const bool in = i < nown && (k >> 20) == th.bin;
-        const uint64_t m = __ballot(in);
-        if (m) {
-          uint32_t b = 0;
-          if (lane == 0) b = atomicAdd(&cs.misc[0], (uint32_t)__popcll(m));
-          b = (uint32_t)__builtin_amdgcn_readlane((int)b, 0);
-          if (in) cs.ck[min(b + lane_rank(m), (uint32_t)kCoopCand - 1u)] = k;  // < kCoopCand by construction
-        }
+      for (int i = t; i < nown; i += kMainThreads) {
+        const uint32_t k = cs.keys[i];
+        if ((k >> 20) == th.bin) atomicAdd(&sub[(k >> 12) & 255u], 1u);
       }
       __syncthreads();
-      const uint32_t cb = th.cnt, room = (uint32_t)P - th.above;
-      uint32_t best = kNoKeys, best_n = 0;
-      for (uint32_t j0 = 0; j0 < cb; j0 += kWave) {
-        const uint32_t j = j0 + (uint32_t)lane;
-        const uint32_t c = j < cb ? cs.ck[j] : 0u;
-        uint32_t gec = 0;
-        for (uint32_t i = 0; i < cb; ++i) gec += (cs.ck[i] >= c) ? 1u : 0u;
-        const bool valid = j < cb && gec <= room;
-        best = min(best, valid ? c : kNoKeys);
-        best_n = max(best_n, valid ? gec : 0u);
-      }
-      best = wave_reduce<1>(best);
-      best_n = wave_reduce<2>(best_n);
-      // no key of the bin fits (ties at its top): start above the bin
-      lo_b = best != kNoKeys ? best : next_bin_key(th.bin);
-      cnt = th.above + (best != kNoKeys ? best_n : 0u);
+      // lane l: sub-bins 255-4l .. 252-4l, top down
+      const uint4 v = reinterpret_cast<const uint4*>(sub)[kWave - 1 - lane];
+      const uint32_t a0 = v.w, a1 = v.z, a2 = v.y, a3 = v.x;
+      const uint32_t lt = a0 + a1 + a2 + a3;
+      const uint32_t c0 = wave_scan_incl<0>(lt) - lt + a0, c1 = c0 + a1, c2 = c1 + a2, c3 = c2 + a3;
+      const uint32_t room = (uint32_t)P - th.above;
+      const uint32_t n_ok = wave_reduce<0>((c0 <= room ? 1u : 0u) + (c1 <= room ? 1u : 0u) +
+                                           (c2 <= room ? 1u : 0u) + (c3 <= room ? 1u : 0u));
+      const uint32_t got = wave_reduce<2>(c3 <= room ? c3 : (c2 <= room ? c2 : (c1 <= room ? c1 : (c0 <= room ? c0 : 0u))));
+      // no sub-bin fits (ties at its top): start above the bin
+      lo_b = n_ok ? (th.bin << 20) | ((256u - n_ok) << 12) : next_bin_key(th.bin);
+      cnt = th.above + got;
     }
   }
 
