@@ -33,10 +33,11 @@ def _layer(dev, lens, seed, pattern=None):
     pt, num_pages = S.make_page_table(lens, seed=seed, device=dev)
     L = S.make_decode_layer(lens, seed=seed + 1, device=dev, page_table=pt, num_pages=num_pages)
     pages = L.index_k.view(num_pages, -1)
-    if pattern == "dup":      # every page repeats one of 8 pages: many equal scores
-        src = pages[:8].clone()
+    if pattern in ("dup", "dup64"):  # every page repeats one of 8 (64) pages: many equal scores
+        nsrc = 8 if pattern == "dup" else 64
+        src = pages[:nsrc].clone()
         for p in range(num_pages):
-            pages[p] = src[p % 8]
+            pages[p] = src[p % nsrc]
     elif pattern == "equal":  # every key and scale identical: all scores equal
         pages[:, :8192] = pages[0, :128].repeat(64)
         pages[:, 8192:].view(torch.float32).fill_(1.0)
@@ -68,6 +69,10 @@ CASES = [
     # 64 rows (the largest batch the length plan covers) and 65 (uniform)
     ([int(x) for x in np.random.default_rng(9).integers(1, 20000, 64)], 9, None),
     ([int(x) for x in np.random.default_rng(10).integers(1, 5000, 65)], 10, None),
+    # long rows of repeated pages: runs of equal keys in the workgroups' list
+    # bins and sub-bins
+    ([131072], 11, "dup"),
+    ([131072, 70000], 12, "dup64"),
 ]
 
 

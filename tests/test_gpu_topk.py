@@ -176,3 +176,16 @@ def test_topk_position_and_sorted_share_scratch(dev):
         torch.cuda.synchronize()
         ref = O.topk_select(s, lens, k, sorted_=sorted_)
         assert np.array_equal(out.cpu().numpy(), ref), f"call {it} sorted={sorted_}"
+
+
+@pytest.mark.parametrize("step", [1 / 8, 1 / 32, 1 / 128, 1 / 1024])
+def test_topk_position_order_rounded_scores_long_rows(dev, step):
+    """Scores rounded to a grid: the workgroups' list bins and their
+    256-way sub-bins hold runs of exact ties, so a list bound may have to
+    start above a whole sub-bin or bin (position order, long rows)."""
+    rng = np.random.default_rng(int(1 / step))
+    print(f"[topk] rounded scores step={step}", flush=True)
+    s = (np.round(rng.standard_normal((3, 131072)) / step) * step).astype(np.float32)
+    pt = np.stack([rng.permutation(4096)[:2048] for _ in range(3)]).astype(np.int32)
+    _check(s, [131072, 100000, 65536], 2048, False, dev)
+    _check(s, [131072, 100000, 65536], 2048, False, dev, pt=pt)
