@@ -463,12 +463,14 @@ static_assert(kCoopKeys <= 65536, "own positions are stored as 16-bit indices");
 
 // Keys a workgroup's list aims to hold: twice its expected share of the K
 // selected keys plus 8.  The list's capacity (a multiple of 4, within the
-// area) adds one more share, so that the threshold bin usually fits whole.
+// area) adds half a share, so that the threshold bin often fits whole (else
+// it is split by sub-bins); every workgroup loads every list after the
+// barrier, so capacity costs load time.
 // A list too short for its workgroup only costs the fallback to the
 // histogram form.
 __host__ __device__ inline int pub_target(int nb, int K) { return 2 * ((K + nb - 1) / nb) + 8; }
 __host__ __device__ inline int pub_stride(int nb, int K) {
-  const int want = pub_target(nb, K) + (K + nb - 1) / nb;
+  const int want = pub_target(nb, K) + ((K + nb - 1) / nb + 1) / 2;
   return min((want + 3) & ~3, (kPubWords / nb) & ~3);
 }
 
