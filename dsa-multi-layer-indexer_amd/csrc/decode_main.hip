@@ -1107,6 +1107,28 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
   // entries in position order: thread t takes contiguous entries.  A row of
   // <= K tokens publishes nothing and takes every finite key instead. ----
   const int n_e = all ? nown : (int)cnt;
+  const auto slot_of = [&](int p) {  // a position, or its KV slot when there is a page table
+    if (TOPK && !pt_row) return p;
+    return (pts_lds ? pts[(p >> 6) - pg0] : pt_row[p >> 6]) * DSA_PAGE_TOKENS + (p & (DSA_PAGE_TOKENS - 1));
+  };
+  if (!all && n_e <= kWave) {
+    // a list of at most one wave's entries: wave 0 emits it, ranks by ballot
+    if (wv == 0) {
+      const bool in = lane < n_e;
+      const int i = in ? (int)lpos[lane] : 0;
+      const uint32_t k = in ? cs.keys[i] : 0u;
+      const uint64_t below = (1ull << lane) - 1ull;
+      const bool tie = in && tfin && k == tstar;
+      const uint32_t tr = ties_before + (uint32_t)__popcll(__ballot(tie) & below);
+      const bool sel = in && key_is_finite(k) && (k > tstar || (tie && tr < need3));
+      const uint32_t pos = base + (uint32_t)__popcll(__ballot(sel) & below);
+      if (sel) o[min(pos, (uint32_t)K - 1u)] = slot_of(p_lo + i);  // < K by construction
+    }
+    if (bid == nb - 1)
+      for (int j = (int)nsel + t; j < K; j += kMainThreads) o[j] = TOPK ? S.pad : -1;
+    dbg_stamp(dbk, 11);
+    return;
+  }
   const int per = (n_e + kMainThreads - 1) / kMainThreads;
   const int e0 = min(n_e, t * per), e1 = min(n_e, e0 + per);
   const auto entry = [&](int e) { return all ? e : (int)lpos[e]; };  // -> own position index
@@ -1143,10 +1165,7 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
       const uint32_t k = cs.keys[i];
       const bool tie = tfin && k == tstar;
       if (key_is_finite(k) && (all || k > tstar || (tie && tr < need3))) {
-        const int p = p_lo + i;
-        int v = p;  // a position, or its KV slot when there is a page table
-        if (!TOPK || pt_row) v = (pts_lds ? pts[(p >> 6) - pg0] : pt_row[p >> 6]) * DSA_PAGE_TOKENS + (p & (DSA_PAGE_TOKENS - 1));
-        o[min(pos++, (uint32_t)K - 1u)] = v;  // < K by construction
+        o[min(pos++, (uint32_t)K - 1u)] = slot_of(p_lo + i);  // < K by construction
       }
       tr += tie ? 1u : 0u;
     }
