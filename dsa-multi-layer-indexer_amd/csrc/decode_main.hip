@@ -837,7 +837,8 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
       uint32_t c = 0;
       for (int i = i0; i < i1; ++i) c += cs.keys[i] >= lo_b ? 1u : 0u;
       uint32_t tot;
-      uint32_t off = block_exclusive_scan(c, cs.wave_tmp, &tot);  // tot == cnt
+      // no closing barrier: wave_tmp is next written after the group barrier
+      uint32_t off = block_exclusive_scan<false>(c, cs.wave_tmp, &tot);  // tot == cnt
       for (int i = i0; i < i1; ++i) {
         const uint32_t k = cs.keys[i];
         if (k >= lo_b) {

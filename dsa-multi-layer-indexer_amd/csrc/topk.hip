@@ -77,6 +77,9 @@ __host__ __device__ inline long row_scratch_words(int slab) {
 
 // Exclusive prefix sum over the block (thread order); *total gets the sum.
 // wave_tmp holds one word per wave.
+// TRAIL = false drops the closing barrier: the caller then guarantees a
+// block barrier before wave_tmp is written again.
+template <bool TRAIL = true>
 __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* wave_tmp, uint32_t* total) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wv = threadIdx.x / kWave;
@@ -90,7 +93,7 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* w
     before += (i < wv) ? x : 0u;
     tot += x;
   }
-  __syncthreads();
+  if constexpr (TRAIL) __syncthreads();
   *total = tot;
   return before + inc - v;
 }
