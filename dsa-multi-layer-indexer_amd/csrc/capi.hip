@@ -93,8 +93,8 @@ int check_mla(const void* q_bf16, const void* kv_pool, int64_t kv_rows, const in
   return DSA_OK;
 }
 
-int resolve_nsplit(int nsplit, int topk) {
-  return nsplit > 0 ? nsplit : dsa::attn_auto_nsplit(topk);
+int resolve_nsplit(int nsplit, int topk, int B, int H) {
+  return nsplit > 0 ? nsplit : dsa::attn_auto_nsplit(topk, B, H);
 }
 
 // in_schedule: attend_idx == NULL is resolved by the MLI schedule (the most
@@ -132,7 +132,7 @@ dsa::AttnArgs attn_args(const void* q_bf16, const void* kv_pool, int64_t kv_rows
   A.out = (uint16_t*)out_bf16;
   A.H = H;
   A.topk = topk;
-  A.nsplit = resolve_nsplit(nsplit, topk);
+  A.nsplit = resolve_nsplit(nsplit, topk, B, H);
   A.sm_log2 = sm_scale * 1.4426950408889634f;
   dsa::attn_bind_workspace(A, workspace, B);
   return A;

@@ -57,7 +57,7 @@ void set_scan_variant(int v);
 void set_coop_select(int on);
 void set_scan_blocks_cap(int n);
 int group_wait_timeouts(int reset);
-int attn_auto_nsplit(int topk);
+int attn_auto_nsplit(int topk, int B, int H);
 int attn_fused_nsplit(int topk, int B, int H);
 size_t attn_workspace_bytes(int B, int H, int nsplit);
 void attn_bind_workspace(AttnArgs& A, void* ws, int B);

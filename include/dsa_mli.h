@@ -178,10 +178,13 @@ typedef struct dsa_layer_args {
   int B, Hidx, H, topk, nsplit, pt_stride, slab_stride;
   float sm_scale;
 } dsa_layer_args;
-/* nsplit = 0: automatic.  The attention of a layer launch that also scans
- * (the lagged case) takes one 128-key tile per split, capped so its
- * workgroups hold about a quarter of the CUs (large batches then scan beside
- * them); the attention launched alone takes one tile per split. */
+/* nsplit = 0: automatic.  The attention launched alone takes one split per
+ * 64 selected keys, at most one workgroup per CU over the batch's (row, head
+ * group)s; the attention of a layer launch that also scans (the lagged case)
+ * takes the same, capped so its workgroups hold about a quarter of the CUs
+ * (large batches then scan beside them).  The split count is part of the
+ * arithmetic: outputs at different split counts agree to rounding, not
+ * bitwise. */
 
 int dsa_decode_layer(const dsa_layer_args* args, void* stream);
 

@@ -29,8 +29,10 @@ def _stack(dev, n_layers=3, indexer_every=1):
     from lagged_indexer_dsa_amd import synthetic as S
 
     pt, num_pages = S.make_page_table(LENS, seed=1, device=dev)
+    # a fixed split count: the shared launch and the standalone attention
+    # would otherwise pick their own (the split count is part of the rounding)
     layers = [S.make_decode_layer(LENS, seed=10 + i, device=dev, page_table=pt, num_pages=num_pages,
-                                  indexer=(i % indexer_every == 0))
+                                  indexer=(i % indexer_every == 0), nsplit=16)
               for i in range(n_layers)]
     first = S.random_selection(LENS, 2048, pt, seed=99, device=dev)
     return layers, first, pt
@@ -80,7 +82,7 @@ def test_decode_layer_composite_matches_ops_and_oracle(dev):
     sc = L.scores.cpu().numpy()
     ref_sel = O.topk_select(sc, np.array(LENS), 2048, page_table=pt.cpu().numpy())
     assert np.array_equal(L.next_idx.cpu().numpy(), ref_sel)
-    out = ops.sparse_mla_decode(L.q_bf16, L.kv_pool, L.next_idx)
+    out = ops.sparse_mla_decode(L.q_bf16, L.kv_pool, L.next_idx, nsplit=L.nsplit)
     torch.cuda.synchronize()
     assert _eq(out, L.out)
 
@@ -129,10 +131,10 @@ def test_mli_layer_attends_previous_selection(dev):
     MLISchedule(layers, first).run_eager()
     torch.cuda.synchronize()
     for i in range(1, 3):
-        o = ops.sparse_mla_decode(layers[i].q_bf16, layers[i].kv_pool, layers[i - 1].next_idx)
+        o = ops.sparse_mla_decode(layers[i].q_bf16, layers[i].kv_pool, layers[i - 1].next_idx, nsplit=16)
         torch.cuda.synchronize()
         assert _eq(o, layers[i].out)
-    o0 = ops.sparse_mla_decode(layers[0].q_bf16, layers[0].kv_pool, first)
+    o0 = ops.sparse_mla_decode(layers[0].q_bf16, layers[0].kv_pool, first, nsplit=16)
     torch.cuda.synchronize()
     assert _eq(o0, layers[0].out)
 
@@ -150,7 +152,7 @@ def test_mli_lag_depth_and_indexcache_pattern(dev, depth, pattern, cold):
     print(f"[mli] depth={depth} pattern={pattern} cold={cold}", flush=True)
     pt, num_pages = S.make_page_table(LENS, seed=1, device=dev)
     layers = [S.make_decode_layer(LENS, seed=40 + i, device=dev, page_table=pt, num_pages=num_pages,
-                                  indexer=(c == "F"))
+                                  indexer=(c == "F"), nsplit=16)
               for i, c in enumerate(pattern)]
     first = layers[0].next_idx if cold else S.random_selection(LENS, 2048, pt, seed=98, device=dev)
     src = O.mli_attend_sources([c == "F" for c in pattern], 0 if cold else -1, depth)
