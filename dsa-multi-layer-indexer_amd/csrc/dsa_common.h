@@ -194,6 +194,7 @@ __device__ __forceinline__ uint32_t load_dev4(__amdgpu_buffer_rsrc_t r, uint32_t
 extern __device__ int g_group_wait_timeouts;
 constexpr int kGroupSpinMax = 1 << 20;
 constexpr int kGroupSyncGroups = 16, kGroupSyncFlags = 8, kGroupSyncLine = 64;
+constexpr int kGroupFlatMax = 32;  // groups up to this size use one arrival counter
 __device__ __forceinline__ uint32_t group_sense(const uint32_t* sync, int bid) {
   return __hip_atomic_load(&sync[(kGroupSyncGroups + 1 + (bid & (kGroupSyncFlags - 1))) * kGroupSyncLine],
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -202,12 +203,15 @@ __device__ __forceinline__ void group_barrier(uint32_t* sync, int bid, int nb, u
   wait_mem();
   __syncthreads();
   if (threadIdx.x == 0) {
-    const int g = bid % kGroupSyncGroups;
-    const uint32_t ng = (uint32_t)((nb - 1 - g) / kGroupSyncGroups + 1);
+    // a small group arrives on one counter (one atomic round trip); a large
+    // one on kGroupSyncGroups counters, whose last arrivals meet on a top one
+    const int ngrp = nb <= kGroupFlatMax ? 1 : kGroupSyncGroups;
+    const int g = bid % ngrp;
+    const uint32_t ng = (uint32_t)((nb - 1 - g) / ngrp + 1);
     bool last = false;
     if (atomicAdd(&sync[g * kGroupSyncLine], 1u) == ng - 1u) {
-      const uint32_t ngroups = (uint32_t)min(nb, kGroupSyncGroups);
-      last = atomicAdd(&sync[kGroupSyncGroups * kGroupSyncLine], 1u) == ngroups - 1u;
+      const uint32_t ngroups = (uint32_t)min(nb, ngrp);
+      last = ngrp == 1 || atomicAdd(&sync[kGroupSyncGroups * kGroupSyncLine], 1u) == ngroups - 1u;
     }
     if (last) {
       // re-zero the counters for the next launch (each barrier is used once
