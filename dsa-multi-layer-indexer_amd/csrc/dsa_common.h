@@ -184,7 +184,8 @@ __device__ __forceinline__ uint32_t load_dev4(__amdgpu_buffer_rsrc_t r, uint32_t
 // use).  Every member publishes (device-scope stores, waited for) and
 // arrives on its group's counter (member bid -> group bid % 16, so each line
 // sees few atomics); the last of a group arrives on the top counter; the
-// last of all re-zeroes the counters and flips the flags.  The others spin
+// last of all re-zeroes the counters and flips the flags.  A group of at
+// most kGroupFlatMax members arrives on counter 0 alone.  The others spin
 // on the flag of their XCD (bid % 8), reading it with device-scope loads.
 // `sense` is the flags' value before this barrier (read at launch start;
 // the flags flip once per use).  The wait is bounded (about a second): on
