@@ -188,13 +188,20 @@ int enqueue_layer(const dsa_layer_args* a, const int32_t* attend, bool with_inde
   int rc;
   if (with_indexer && a->B >= kSplitLaunchRows) {
     // large batches: a plain scan launch (two workgroups per CU) writes the
-    // scores, then the select loads them beside the attention
+    // scores, a select launch loads them, then the attention runs alone at
+    // its own split count (sharing a launch, each role would hold one
+    // workgroup per CU and starve the other)
     dsa::ScanArgs P = S;
     P.next_idx = nullptr;
     P.hist = nullptr;
     rc = hip_status(dsa::launch_decode_main(nullptr, 0, &P, a->B, s), "indexer scan launch");
     if (rc) return rc;
     S.from_scores = 1;
+    rc = hip_status(dsa::launch_decode_main(nullptr, 0, &S, a->B, s), "top-k select launch");
+    if (rc || !attention) return rc;
+    if (a->nsplit <= 0) A = attn_args(a->q_bf16, a->kv_pool, a->kv_rows, attend, a->workspace, a->out_bf16,
+                                      a->B, a->H, a->topk, 0, a->sm_scale);
+    return hip_status(dsa::launch_decode_main(&A, a->B, nullptr, 0, s), "attention launch");
   }
   rc = hip_status(dsa::launch_decode_main(attention && !own ? &A : nullptr, a->B, with_indexer ? &S : nullptr,
                                           a->B, s),

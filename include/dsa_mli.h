@@ -148,8 +148,8 @@ int dsa_sparse_mla_decode(const void* q_bf16, const void* kv_pool,
  * (4) One DSA decode layer on one stream:
  *   indexer scan -> top-k (position order, KV-slot output into next_idx),
  *   and attention over attend_idx (the lagged set: the attention and the
- *   scan then share ONE launch; from B = 8 rows the scan is a launch of its
- *   own and the select shares the attention's), or over this layer's own
+ *   scan then share ONE launch; from B = 8 rows the scan, the select and
+ *   the attention are three launches in that order), or over this layer's own
  *   fresh selection when attend_idx == NULL (baseline DSA: scan, select,
  *   then attention).
  * scores [B, slab_stride] fp32 scratch; next_idx [B, topk] int32.
@@ -182,7 +182,7 @@ typedef struct dsa_layer_args {
  * 64 selected keys, at most one workgroup per CU over the batch's (row, head
  * group)s; the attention of a layer launch that also scans (the lagged case)
  * takes the same, capped so its workgroups hold about a quarter of the CUs
- * (large batches then scan beside them).  The split count is part of the
+ * (in a launch shared with the scan).  The split count is part of the
  * arithmetic: outputs at different split counts agree to rounding, not
  * bitwise. */
 
@@ -193,8 +193,8 @@ int dsa_decode_layer(const dsa_layer_args* args, void* stream);
  * Layer i attends the selection of the most recent earlier layer that runs
  * an indexer (its attend_idx when given; layer 0 must be given one), and
  * layer i's indexer scan runs in the SAME launch as layer i's attention
- * (role-decoupled workgroups; from B = 8 rows the scan runs just before it
- * and the select shares the attention's launch), followed by layer i's
+ * (role-decoupled workgroups; from B = 8 rows scan, select and attention
+ * are three launches), followed by layer i's
  * top-k select, which layer i+1 attends.  A layer whose q_fp8 is NULL runs no indexer (IndexCache
  * reuse); one whose q_bf16 is NULL runs no attention.  Everything is on one
  * stream: the overlap of indexer and attention is inside each launch.

@@ -177,8 +177,8 @@ def test_mli_lag_depth_and_indexcache_pattern(dev, depth, pattern, cold):
 
 
 def test_mli_large_batch_two_launch_layers_equal_serial(dev):
-    """>= 8 rows: each indexer layer is a scan launch and a select launch
-    (beside the attention); outputs and selections equal the standalone ops."""
+    """>= 8 rows: each indexer layer is a scan launch, a select launch and an
+    attention launch; outputs and selections equal the standalone ops."""
     from lagged_indexer_dsa_amd import synthetic as S
     from lagged_indexer_dsa_amd.decode import MLISchedule
 
