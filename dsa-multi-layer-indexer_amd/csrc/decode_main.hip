@@ -857,7 +857,7 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
     }
   }
   dbg_stamp(dbk, 8);
-  group_barrier(sync, bid, nb, cs.sense[0]);
+  group_barrier_rep(sync, sync + 3 * kSyncWords, bid, nb, cs.sense[0]);
   dbg_stamp(dbk, 9);
 
   // ---- every workgroup: all lists into registers (one batch of

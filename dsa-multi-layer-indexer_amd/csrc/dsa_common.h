@@ -200,6 +200,52 @@ __device__ __forceinline__ uint32_t group_sense(const uint32_t* sync, int bid) {
   return __hip_atomic_load(&sync[(kGroupSyncGroups + 1 + (bid & (kGroupSyncFlags - 1))) * kGroupSyncLine],
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// A group barrier with one atomic round trip on the last arrival's path.
+// Members arrive on kRepGroups group counters; a group's last arrival adds
+// itself, without waiting for the result, to kRepTops replicated top
+// counters, and every member polls the replica of its XCD until all groups
+// are in.  Two counter sets alternate by launch (`sense`, the flags of
+// `sync` read at launch start), so nothing is re-zeroed while a member may
+// still read it: after passing, workgroup 0 clears the other set (the next
+// launch's) and flips the flags.  Layout: set s's group counters on lines
+// 8s..8s+7 of `sync`, its top replicas on lines 8s..8s+7 of `tops` (a second
+// barrier area), the flags where group_barrier keeps them.
+constexpr int kRepGroups = 8, kRepTops = 8;
+static_assert(2 * kRepGroups <= kGroupSyncGroups && 2 * kRepTops <= kGroupSyncGroups + 1,
+              "two counter sets fit a barrier area");
+__device__ __forceinline__ void group_barrier_rep(uint32_t* sync, uint32_t* tops, int bid, int nb,
+                                                  uint32_t sense) {
+  const uint32_t set = sense & 1u;
+  wait_mem();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int g = bid % kRepGroups;
+    const uint32_t ng = (uint32_t)((nb - 1 - g) / kRepGroups + 1);
+    if (atomicAdd(&sync[(set * kRepGroups + g) * kGroupSyncLine], 1u) == ng - 1u)
+      for (int r = 0; r < kRepTops; ++r)
+        __hip_atomic_fetch_add(&tops[(set * kRepTops + r) * kGroupSyncLine], 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t ngroups = (uint32_t)min(nb, kRepGroups);
+    const uint32_t* top = &tops[(set * kRepTops + bid % kRepTops) * kGroupSyncLine];
+    for (int i = 0; __hip_atomic_load(top, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < ngroups; ++i) {
+      if (i == kGroupSpinMax) {
+        atomicAdd(&g_group_wait_timeouts, 1);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  __syncthreads();
+  if (bid == 0) {
+    const int t = threadIdx.x;
+    if (t < kRepGroups) store_dev(&sync[((set ^ 1u) * kRepGroups + t) * kGroupSyncLine], 0u);
+    else if (t < kRepGroups + kRepTops)
+      store_dev(&tops[((set ^ 1u) * kRepTops + (t - kRepGroups)) * kGroupSyncLine], 0u);
+    else if (t < kRepGroups + kRepTops + kGroupSyncFlags)
+      store_dev(&sync[(kGroupSyncGroups + 1 + (t - kRepGroups - kRepTops)) * kGroupSyncLine], sense ^ 1u);
+  }
+}
+
 __device__ __forceinline__ void group_barrier(uint32_t* sync, int bid, int nb, uint32_t sense) {
   wait_mem();
   __syncthreads();

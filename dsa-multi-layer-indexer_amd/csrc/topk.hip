@@ -62,7 +62,7 @@ constexpr int kSyncGroups = 16;
 constexpr int kSyncFlags = 8;
 constexpr int kSyncLine = 64;  // words
 constexpr int kSyncWords = (kSyncGroups + 1 + kSyncFlags) * kSyncLine;
-constexpr int kNumSync = 3;
+constexpr int kNumSync = 4;  // slots 0 and 3: the list barrier (group_barrier_rep)
 static_assert(kSyncGroups == kGroupSyncGroups && kSyncFlags == kGroupSyncFlags && kSyncLine == kGroupSyncLine,
               "group-barrier layout");
 __host__ __device__ inline long row_sync_off(int slab) { return kBmOff + bitmap_words(slab) + 2L * kCandCap; }
