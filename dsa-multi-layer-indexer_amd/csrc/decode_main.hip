@@ -1567,10 +1567,10 @@ int attn_auto_nsplit(int topk, int B, int H) {
   return std::max(1, std::min(cap, (topk + kAutoSplitKeys - 1) / kAutoSplitKeys));
 }
 
-// Splits when the attention shares the launch with indexer scans: one
-// 128-key tile per split, but the attention workgroups together take at most
-// about a quarter of the CUs, so a large batch's scans run beside them
-// (measured at 32 ragged requests: 2 splits 180 us/layer, 16 splits 203).
+// Splits when the attention shares the launch with indexer scans: the
+// default count, but the attention workgroups together take at most about a
+// quarter of the CUs, so the scans keep the rest (at b = 1: 32 splits of 64
+// keys beside 224 scan workgroups).
 int attn_fused_nsplit(int topk, int B, int H) {
   const int groups = std::max(1, B * (H / kHG));
   return std::max(1, std::min(attn_auto_nsplit(topk, B, H), device_cus() / 4 / groups));
