@@ -279,7 +279,7 @@ def main() -> int:
                 att = L.next_idx
     t_serial = time_graph(serial, reps, torch)
 
-    # ---- the standalone ops (scan-only launches, the two-launch top-k, the
+    # ---- the standalone ops (scan-only launches, the top-k (position order: one select launch), the
     # attention alone), each rotating over the sets' first layers ----
     L0s = [ls[0] for ls in sets]
 
