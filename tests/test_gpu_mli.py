@@ -176,7 +176,7 @@ def test_mli_lag_depth_and_indexcache_pattern(dev, depth, pattern, cold):
     sched.close()
 
 
-def test_mli_large_batch_two_launch_layers_equal_serial(dev):
+def test_mli_large_batch_layers_equal_serial(dev):
     """>= 8 rows: each indexer layer is a scan launch, a select launch and an
     attention launch; outputs and selections equal the standalone ops."""
     from lagged_indexer_dsa_amd import synthetic as S
@@ -202,3 +202,26 @@ def test_mli_large_batch_two_launch_layers_equal_serial(dev):
             assert _eq(outs[i], ref_out[i]), f"{mode} layer {i} output"
             assert _eq(sels[i], ref_sel[i]), f"{mode} layer {i} selection"
     sched.close()
+
+
+def test_large_batch_layer_attends_own_selection(dev):
+    """>= 8 rows, attend_idx = NULL (baseline DSA): the attention launch
+    follows the select launch and reads the fresh selection; the selection
+    equals the oracle top-k of the layer's scores, the output equals the
+    standalone attention over it at the default split count."""
+    from lagged_indexer_dsa_amd import ops
+    from lagged_indexer_dsa_amd import synthetic as S
+
+    print("[mli] 9-row own selection", flush=True)
+    lens = [9000, 3000, 2048, 70, 5000, 12000, 800, 4097, 1]
+    pt, num_pages = S.make_page_table(lens, seed=5, device=dev)
+    L = S.make_decode_layer(lens, seed=70, device=dev, page_table=pt, num_pages=num_pages)
+    for rep in range(2):
+        L.out.zero_(); L.next_idx.fill_(-7)
+        L.run(attend_idx=None)
+        torch.cuda.synchronize()
+        ref_sel = O.topk_select(L.scores.cpu().numpy(), np.array(lens), 2048, page_table=pt.cpu().numpy())
+        assert np.array_equal(L.next_idx.cpu().numpy(), ref_sel), f"rep {rep} selection"
+        out = ops.sparse_mla_decode(L.q_bf16, L.kv_pool, L.next_idx)
+        torch.cuda.synchronize()
+        assert _eq(out, L.out), f"rep {rep} output"
