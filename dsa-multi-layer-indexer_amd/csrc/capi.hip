@@ -312,7 +312,9 @@ int dsa_topk(const float* scores, const int32_t* seq_lens, const int32_t* page_t
   hipStream_t s = (hipStream_t)stream;
   if (flags == DSA_TOPK_POSITION_ORDER) {
     // position order: one launch of the decode kernel's select over the given
-    // scores (its workgroups split each row and select together)
+    // scores (its workgroups split each row and select together).  The
+    // select only reads the scores (the score-loading role stores none), so
+    // the caller's const buffer is passed through ScanArgs unchanged.
     dsa::ScanArgs S = scan_args(nullptr, nullptr, nullptr, 0, page_table, seq_lens,
                                 const_cast<float*>(scores), 16,
                                 page_table ? pt_stride : (slab_stride + DSA_PAGE_TOKENS - 1) / DSA_PAGE_TOKENS,
