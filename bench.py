@@ -178,7 +178,7 @@ def main() -> int:
 
     import torch
 
-    from lagged_indexer_dsa_amd import ops
+    from lagged_indexer_dsa_amd import _lib, ops
     from lagged_indexer_dsa_amd import synthetic as S
     from lagged_indexer_dsa_amd.decode import MLISchedule
 
@@ -235,6 +235,7 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
 
+    _lib.sync_timeouts(reset=True)
     for i in range(args.warmup):
         fulls[i % n_sets].replay()
     # ---- timed region: exactly `steps` graph replays, bracketed by one HIP
@@ -249,6 +250,13 @@ def main() -> int:
     ev1.record()
     torch.cuda.synchronize()
     ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    # the fused launches hand data between workgroups through bounded waits;
+    # an expired wait means wrong (and fast) results: refuse to report them
+    n_timeouts = _lib.sync_timeouts()
+    if n_timeouts:
+        print(json.dumps({"error": f"{n_timeouts} in-launch group waits expired in the timed region; "
+                                   "results invalid", "config": cfg["desc"]}), flush=True)
+        return 3
     # every replay is n_layers launches of the one kernel; the figure includes
     # the launch-to-launch gaps, so it bounds the kernel's duration from above
     launch_ms = ev0.elapsed_time(ev1) / (args.steps * n_layers)
@@ -361,7 +369,8 @@ def main() -> int:
                       "indexer_scan_event_pairs": round(scan_ms_pairs * 1e3, 3)},
         "attention_gather_GBps": round(ab / (attn_ms * 1e-3) / 1e9, 1),
         "mli": {"graph_ms": round(t_full, 5), "eager_ms": round(t_eager, 5),
-                "serial_1stream_ms": round(t_serial, 5), "attn_only_ms": round(t_attn, 5),
+                "serial_ms": round(t_attn + t_idx, 5),
+                "eager_layer_calls_ms": round(t_serial, 5), "attn_only_ms": round(t_attn, 5),
                 "indexer_only_ms": round(t_idx, 5),
                 "hidden_fraction": None if hidden is None else round(hidden, 4)},
         "roofline": {"bound": "hbm", "achieved": round(layer_gbs, 1), "peak": HBM_PEAK_GBS,
@@ -370,6 +379,11 @@ def main() -> int:
                      "kernel": "decode_main_kernel (fused layer launch)",
                      "algorithmic_bytes": lb, "launch_us": round(launch_ms * 1e3, 3)},
     }
+    n_timeouts = _lib.sync_timeouts()
+    if n_timeouts:
+        print(json.dumps({"error": f"{n_timeouts} in-launch group waits expired outside the timed region"}),
+              flush=True)
+        return 3
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(131072 if args.config == "c3" else 8192, args.cpu_budget)
     for s in scheds:

@@ -284,7 +284,9 @@ extern "C" {
 
 const char* dsa_last_error(void) { return g_err; }
 
-const char* dsa_version(void) { return "dsa_mli 0.2.0 gfx950"; }
+const char* dsa_version(void) { return "dsa_mli 0.3.0 gfx950"; }
+
+int dsa_sync_timeouts(int reset) { return dsa::group_wait_timeouts(reset); }
 
 int dsa_indexer_scan(const void* q_fp8, const float* w, const void* index_k, int64_t num_pages,
                      const int32_t* page_table, const int32_t* seq_lens, float* scores, int B,

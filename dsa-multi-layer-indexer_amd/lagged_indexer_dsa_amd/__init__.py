@@ -4,7 +4,7 @@ Hot path (HIP kernels for gfx950 behind the C ABI of include/dsa_mli.h):
 lightning-indexer scan over a paged fp8 index-K cache -> exact top-k ->
 split-K sparse MLA over the fp8 656-byte latent pool, and the MLI lag
 schedule (layer i attends layer i-1's selection while layer i's indexer runs
-on a second stream) captured as one hipGraph.
+in the same launch, on workgroups of their own) captured as one hipGraph.
 
 Python surface mirrors the reference package ``lagged_indexer_dsa``
 (attention_core / dsa_layer / model / config); every compute call goes to

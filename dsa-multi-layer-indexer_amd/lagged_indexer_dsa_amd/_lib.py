@@ -67,6 +67,7 @@ _LIB: ctypes.CDLL | None = None
 SIGNATURES = {
     "dsa_last_error": (ctypes.c_char_p, []),
     "dsa_version": (ctypes.c_char_p, []),
+    "dsa_sync_timeouts": (_i32, [_i32]),
     "dsa_indexer_scan": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp]),
     "dsa_topk_scratch_bytes": (ctypes.c_size_t, [_i32, _i32]),
     "dsa_topk": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
@@ -118,3 +119,12 @@ def check(rc: int) -> None:
 
 def call(name: str, *args) -> None:
     check(getattr(load(), name)(*args))
+
+
+def sync_timeouts(reset: bool = False) -> int:
+    """In-launch group waits that expired since load or the last reset
+    (dsa_sync_timeouts); nonzero means some launch's results are wrong."""
+    n = load().dsa_sync_timeouts(1 if reset else 0)
+    if n < 0:
+        raise DsaError(DSA_ERR_HIP, "dsa_sync_timeouts: counter unreadable")
+    return n

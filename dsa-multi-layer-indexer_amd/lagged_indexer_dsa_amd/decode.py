@@ -138,7 +138,9 @@ class MLISchedule:
                   torch.cuda.current_stream().cuda_stream)
 
     def capture(self) -> None:
-        """Capture the whole step into one hipGraph (two streams inside)."""
+        """Capture the whole step into one hipGraph: one stream, one launch
+        per layer (three from 8 rows); the indexer and the attention overlap
+        inside each launch, not across streams."""
         if self._graph is not None:
             return
         h = ctypes.c_void_p()

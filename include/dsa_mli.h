@@ -62,6 +62,26 @@ const char* dsa_last_error(void);
 const char* dsa_version(void);
 
 /*
+ * Count of in-launch group waits that expired on the current device since
+ * the library was loaded (or since the last call with reset != 0); reset != 0
+ * zeroes it after reading.  Returns -1 if the count cannot be read.
+ * Synchronous (waits for the device's queued work to read the counter).
+ *
+ * The cooperative top-k select and the split-K merge hand data between
+ * workgroups of ONE launch through bounded spin waits.  They rely on every
+ * workgroup of a group being resident at once: workgroups are dispatched in
+ * index order and each group is smaller than the device, so this holds when
+ * the launch has the device to itself or shares it only with kernels that
+ * finish without waiting on it.  A wait that expires (about a second) is
+ * counted here and the launch goes on, so a launch that broke the
+ * assumption returns instead of hanging the device -- but its results are
+ * wrong.  A caller that cannot rule out such sharing checks that this count
+ * stays 0.  No counterpart in the reference, whose waits are unbounded
+ * (K:1093-1095, K:2219-2224).
+ */
+int dsa_sync_timeouts(int reset);
+
+/*
  * (1) Lightning-indexer scan.
  *   scores[b, g] = kscale[g] * sum_h w[b,h] * ReLU( sum_d q[b,h,d] * k[g,d] )
  * for g < seq_lens[b]; scores[b, g] = -inf for seq_lens[b] <= g < slab_stride.

@@ -1,0 +1,195 @@
+"""GPU: the exact path bench.py times, at its own shape, against the oracle.
+
+C3: ctx 131072, b = 1, 64x128 indexer, 16 heads,
+top-2048, two layers under the MLI lag captured as one hipGraph, each layer
+ONE fused launch (attention over the lagged set + scan + cooperative select),
+at the library's default split count (nsplit = 0), built exactly as bench.py
+builds a layer set.  After each of several replays, for each layer:
+  * the score slab equals the oracle's fp8-semantics scores (rel 1e-4 of the
+    row's max |score|, -inf tail exact);
+  * next_idx equals the oracle's top-2048 of those scores mapped to KV slots,
+    bit-exact (lower index wins ties; K:1097-1144);
+  * out equals the oracle's sparse MLA over the set the layer attended
+    (rel 2e-2 of max |out|, the north-star tolerance; K:3104);
+  * no in-launch group wait expired (dsa_sync_timeouts == 0).
+Reference: model.py:116-127 (LAGGED_FUSED), K:3072-3365 (validate gates).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import dsa_oracle as O
+
+from _cases import rel_err
+
+pytestmark = pytest.mark.gpu
+
+C3_LENS = [131072]
+
+
+def _oracle_scores_row(L, b: int, n: int) -> np.ndarray:
+    """Oracle scores of row b, reading only that row's pages."""
+    npg = (n + 63) // 64
+    pt_row = L.page_table[b, :npg].long()
+    pages = L.index_k[pt_row].cpu().numpy()
+    local_pt = np.arange(npg, dtype=np.int32)[None, :]
+    return O.indexer_scores(L.q_fp8[b:b + 1].cpu().numpy(), L.w[b:b + 1].cpu().numpy(), pages,
+                            local_pt, np.array([n]), n)[0]
+
+
+def _oracle_attention_row(L, b: int, att: torch.Tensor) -> np.ndarray:
+    """Oracle sparse MLA of row b over the KV slots att[b] (gathering only
+    those rows)."""
+    sl = att[b].long()
+    valid = (sl >= 0) & (sl < L.kv_pool.shape[0])
+    rows = L.kv_pool[sl[valid]].cpu().numpy()
+    idx = np.arange(rows.shape[0], dtype=np.int32)[None, :]
+    q = L.q_bf16[b:b + 1].float().cpu().numpy()
+    return O.sparse_mla_decode(q, rows, idx, L.sm_scale)[0]
+
+
+def check_layer(L, att: torch.Tensor, rows, lens, tag: str) -> None:
+    torch.cuda.synchronize()
+    pt = L.page_table.cpu().numpy()
+    sc = L.scores.cpu().numpy()
+    if L.has_indexer:
+        ref_sel = O.topk_select(sc, np.array(lens), L.topk, page_table=pt)
+        got = L.next_idx.cpu().numpy()
+        bad = np.nonzero((got != ref_sel).any(1))[0]
+        assert bad.size == 0, f"{tag}: selection differs on rows {bad[:4]}"
+    out = L.out.float().cpu().numpy()
+    for b in rows:
+        n = lens[b]
+        if L.has_indexer:
+            ref = _oracle_scores_row(L, b, n)
+            err = rel_err(sc[b, :n], ref)
+            assert err < 1e-4, f"{tag} row {b}: scan rel err {err:.2e}"
+            assert np.all(np.isneginf(sc[b, n:])), f"{tag} row {b}: tail not -inf"
+        ref_o = _oracle_attention_row(L, b, att)
+        err = rel_err(out[b], ref_o)
+        assert err < 2e-2, f"{tag} row {b}: attention rel err {err:.2e}"
+
+
+def test_c3_bench_graph_matches_oracle(dev):
+    from lagged_indexer_dsa_amd import _lib
+    from lagged_indexer_dsa_amd import synthetic as S
+    from lagged_indexer_dsa_amd.decode import MLISchedule
+
+    print("[bench-path] C3 131072 x 2 layers, graph", flush=True)
+    _lib.sync_timeouts(reset=True)
+    pt, num_pages = S.make_page_table(C3_LENS, seed=1000, device=dev)
+    layers = [S.make_decode_layer(C3_LENS, seed=3000 + i, device=dev, page_table=pt, num_pages=num_pages)
+              for i in range(2)]
+    first = S.random_selection(C3_LENS, 2048, pt, seed=7, device=dev)
+    sched = MLISchedule(layers, first)
+    sched.capture()
+    first_out = None
+    for rep in range(3):
+        for L in layers:
+            L.out.zero_(); L.next_idx.fill_(-7); L.scores.fill_(7.0)
+        torch.cuda.synchronize()
+        print(f"[bench-path] replay {rep}", flush=True)
+        sched.replay()
+        torch.cuda.synchronize()
+        assert _lib.sync_timeouts() == 0, "a group wait expired"
+        check_layer(layers[0], first, [0], C3_LENS, f"replay {rep} layer 0")
+        check_layer(layers[1], layers[0].next_idx, [0], C3_LENS, f"replay {rep} layer 1")
+        outs = [L.out.clone() for L in layers]
+        if first_out is None:
+            first_out = outs
+        else:  # replays are deterministic
+            for a, b in zip(first_out, outs):
+                assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+        _ = torch.randn(1000, device=dev).sum().item()  # eager work between replays
+    sched.close()
+    assert _lib.sync_timeouts() == 0
+
+
+def c4_lens() -> list[int]:
+    """32 requests, ctx uniform in [16384, 131072],
+    drawn as bench.py draws them (seed 4000)."""
+    g = torch.Generator().manual_seed(4000)
+    return torch.randint(16384, 131073, (32,), generator=g).tolist()
+
+
+@pytest.mark.parametrize("mode", ["eager", "graph"])
+def test_c4_varlen32_matches_oracle(dev, mode):
+    """C4: 32 ragged rows (~2.4M tokens) through the MLI schedule (scan,
+    select and attention launches per layer).  Every row's selection is
+    bit-exact; scores and outputs are checked on 4 rows including the
+    longest and the shortest."""
+    from lagged_indexer_dsa_amd import _lib
+    from lagged_indexer_dsa_amd import synthetic as S
+    from lagged_indexer_dsa_amd.decode import MLISchedule
+
+    lens = c4_lens()
+    print(f"[bench-path] C4 {mode} sum={sum(lens)}", flush=True)
+    _lib.sync_timeouts(reset=True)
+    pt, num_pages = S.make_page_table(lens, seed=1000, device=dev)
+    layers = [S.make_decode_layer(lens, seed=3000 + i, device=dev, page_table=pt, num_pages=num_pages)
+              for i in range(2)]
+    first = S.random_selection(lens, 2048, pt, seed=7, device=dev)
+    sched = MLISchedule(layers, first)
+    rows = sorted({int(np.argmax(lens)), int(np.argmin(lens)), 0, 17})
+    for rep in range(2):
+        for L in layers:
+            L.out.zero_(); L.next_idx.fill_(-7)
+        torch.cuda.synchronize()
+        sched.run_eager() if mode == "eager" else sched.replay()
+        torch.cuda.synchronize()
+        assert _lib.sync_timeouts() == 0, "a group wait expired"
+        check_layer(layers[0], first, rows, lens, f"{mode} rep {rep} layer 0")
+        check_layer(layers[1], layers[0].next_idx, rows, lens, f"{mode} rep {rep} layer 1")
+    sched.close()
+    del layers
+    torch.cuda.empty_cache()
+
+
+def test_c5_61_layers_indexcache_matches_oracle(dev):
+    """C5: 196,608 tokens, 61 attention layers, a fresh indexer every 4th
+    layer (IndexCache 1/4) with the MLI lag, one hipGraph.  Every layer's
+    output equals the standalone attention over the selection the oracle's
+    schedule names for it (bitwise, same split count), every fresh selection
+    equals the oracle top-k of its scores, and two layers (the first fresh
+    indexer after layer 0 and a reuse layer) match the oracle end to end."""
+    from lagged_indexer_dsa_amd import _lib, ops
+    from lagged_indexer_dsa_amd import synthetic as S
+    from lagged_indexer_dsa_amd.decode import MLISchedule
+
+    lens = [196608]
+    n_layers, every = 61, 4
+    print("[bench-path] C5 196608 x 61 layers", flush=True)
+    _lib.sync_timeouts(reset=True)
+    pt, num_pages = S.make_page_table(lens, seed=1000, device=dev)
+    produces = O.indexcache_produces(n_layers, freq=every)
+    layers = [S.make_decode_layer(lens, seed=5000 + i, device=dev, page_table=pt, num_pages=num_pages,
+                                  indexer=produces[i])
+              for i in range(n_layers)]
+    first = S.random_selection(lens, 2048, pt, seed=7, device=dev)
+    src = O.mli_attend_sources(produces, -1, 1)
+    sched = MLISchedule(layers, first)
+    sched.capture()
+    for L in layers:
+        L.out.zero_(); L.next_idx.fill_(-7)
+    torch.cuda.synchronize()
+    sched.replay()
+    torch.cuda.synchronize()
+    assert _lib.sync_timeouts() == 0, "a group wait expired"
+    sels = {i: L.next_idx.clone() for i, L in enumerate(layers) if L.has_indexer}
+    for i, L in enumerate(layers):
+        if L.has_indexer:
+            ref_sel = O.topk_select(L.scores.cpu().numpy(), np.array(lens), L.topk, page_table=pt.cpu().numpy())
+            assert np.array_equal(sels[i].cpu().numpy(), ref_sel), f"layer {i} selection"
+        att = first if src[i] == -1 else sels[src[i]]
+        # the split count the schedule's launch used: 32 at b = 1 for both the
+        # fused and the attention-only launch
+        ref = ops.sparse_mla_decode(L.q_bf16, L.kv_pool, att, nsplit=32)
+        torch.cuda.synchronize()
+        assert torch.equal(ref.view(torch.int16), L.out.view(torch.int16)), f"layer {i} attends layer {src[i]}"
+    for i in (4, 5):
+        att = first if src[i] == -1 else sels[src[i]]
+        check_layer(layers[i], att, [0], lens, f"C5 layer {i}")
+    sched.close()
