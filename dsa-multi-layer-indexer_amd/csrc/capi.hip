@@ -8,6 +8,7 @@
 #include <stdio.h>
 
 #include <algorithm>
+#include <mutex>
 #include <vector>
 
 #include "dsa_common.h"
@@ -77,8 +78,8 @@ int check_topk(const float* scores, const int32_t* seq_lens, const int32_t* page
 
 int check_mla(const void* q_bf16, const void* kv_pool, int64_t kv_rows, const int32_t* idx,
               const void* workspace, const void* out_bf16, int B, int H, int topk, int nsplit,
-              bool idx_required = true) {
-  DSA_REQUIRE(q_bf16 && kv_pool && (idx || !idx_required) && workspace && out_bf16,
+              bool idx_required = true, bool ws_required = true) {
+  DSA_REQUIRE(q_bf16 && kv_pool && (idx || !idx_required) && (workspace || !ws_required) && out_bf16,
               DSA_ERR_INVALID_ARG, "dsa_sparse_mla_decode: null pointer argument");
   DSA_REQUIRE(B >= 1 && B <= 65535, DSA_ERR_INVALID_ARG, "dsa_sparse_mla_decode: bad B %d", B);
   DSA_REQUIRE(H >= 16 && H % 16 == 0 && H <= 16 * 64, DSA_ERR_UNSUPPORTED,
@@ -87,7 +88,7 @@ int check_mla(const void* q_bf16, const void* kv_pool, int64_t kv_rows, const in
   DSA_REQUIRE(nsplit >= 0 && nsplit <= 128, DSA_ERR_UNSUPPORTED,
               "dsa_sparse_mla_decode: nsplit must be in [0, 128] (got %d)", nsplit);
   DSA_REQUIRE(kv_rows >= 1, DSA_ERR_INVALID_ARG, "dsa_sparse_mla_decode: kv_rows must be >= 1");
-  DSA_REQUIRE(aligned16(q_bf16) && aligned16(kv_pool) && aligned16(workspace) &&
+  DSA_REQUIRE(aligned16(q_bf16) && aligned16(kv_pool) && (aligned16(workspace) || !ws_required) &&
                   ((uintptr_t)out_bf16 & 7) == 0,
               DSA_ERR_INVALID_ARG, "dsa_sparse_mla_decode: q/kv_pool/workspace must be 16-byte aligned");
   return DSA_OK;
@@ -275,6 +276,46 @@ int check_mli(const dsa_layer_args* layers, int n, int depth) {
 
 }  // namespace
 
+// ---- allocation-free sparse MLA: the split workspace in a static device
+// array.  Layout: kNoAllocGroups group barriers at fixed offsets (so a call of
+// one shape never writes partials over the barriers another shape uses; the
+// array is zero at load, and every launch leaves its barriers re-armed),
+// then the split partials of the current call.  One copy per device; calls
+// that overlap in time on one device race on it. ----
+constexpr int kNoAllocGroups = 512;  // (row, head group) pairs per call
+constexpr size_t kNoAllocSyncBytes = (size_t)kNoAllocGroups * dsa::kSyncWords * sizeof(uint32_t);
+constexpr size_t kNoAllocPartialBytes = (size_t)16 << 20;
+constexpr size_t kNoAllocScratchBytes = kNoAllocSyncBytes + kNoAllocPartialBytes;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+constexpr int kNoAllocMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kNoAllocMaxDevices] = {};
+
+// The device address of `scratch` on the current device, looked up once per
+// device (with that device current).  The array's name in host code is only
+// a host-side handle; kernels must be given this address.
+int scratch_ptr(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+  DSA_REQUIRE(dev >= 0 && dev < kNoAllocMaxDevices, DSA_ERR_UNSUPPORTED, "device %d beyond %d", dev,
+              kNoAllocMaxDevices);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_status(e, "hipGetSymbolAddress(scratch)");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return DSA_OK;
+}
+
+}  // namespace
+
 struct dsa_mli_graph {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
@@ -349,6 +390,32 @@ int dsa_sparse_mla_decode(const void* q_bf16, const void* kv_pool, int64_t kv_ro
                               nsplit, sm_scale);
   return hip_status(dsa::launch_decode_main(&A, B, nullptr, 0, (hipStream_t)stream),
                     "sparse MLA launch");
+}
+
+int dsa_sparse_mla_decode_noalloc(const void* q_bf16, const void* kv_pool, int64_t kv_rows,
+                                  const int32_t* idx, void* out_bf16, int B, int H, int topk, int nsplit,
+                                  float sm_scale, void* stream) {
+  int rc = check_mla(q_bf16, kv_pool, kv_rows, idx, nullptr, out_bf16, B, H, topk, nsplit, true,
+                     /*ws_required=*/false);
+  if (rc) return rc;
+  const int groups = B * (H / 16);
+  const int ns = resolve_nsplit(nsplit, topk, B, H);
+  const size_t part = dsa::attn_workspace_bytes(B, H, ns) - (size_t)groups * dsa::kSyncWords * sizeof(uint32_t);
+  DSA_REQUIRE(groups <= kNoAllocGroups, DSA_ERR_UNSUPPORTED,
+              "dsa_sparse_mla_decode_noalloc: B*H/16 = %d above the static limit %d", groups, kNoAllocGroups);
+  DSA_REQUIRE(part <= kNoAllocPartialBytes, DSA_ERR_UNSUPPORTED,
+              "dsa_sparse_mla_decode_noalloc: %zu partial bytes (B=%d, H=%d, nsplit=%d) above the static %zu",
+              part, B, H, ns, kNoAllocPartialBytes);
+  void* base = nullptr;
+  rc = scratch_ptr(&base);
+  if (rc) return rc;
+  dsa::AttnArgs A = attn_args(q_bf16, kv_pool, kv_rows, idx, base, out_bf16, B, H, topk, ns, sm_scale);
+  // barriers stay at their fixed offsets; the partials follow all of them
+  A.sync = reinterpret_cast<uint32_t*>(base);
+  A.part_o = reinterpret_cast<float*>(static_cast<unsigned char*>(base) + kNoAllocSyncBytes);
+  A.part_ml = A.part_o + (size_t)groups * ns * 16 * DSA_LATENT_DIM;
+  return hip_status(dsa::launch_decode_main(&A, B, nullptr, 0, (hipStream_t)stream),
+                    "sparse MLA (no-alloc) launch");
 }
 
 int dsa_decode_layer(const dsa_layer_args* args, void* stream) {

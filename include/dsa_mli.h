@@ -165,6 +165,26 @@ int dsa_sparse_mla_decode(const void* q_bf16, const void* kv_pool,
                           float sm_scale, void* stream);
 
 /*
+ * (3b) The same sparse MLA decode with no workspace argument and no
+ * allocation: the split partials and the per-(row, head group) barriers live
+ * in a static device array of the library (one copy per device, about 19 MB,
+ * held until the process ends), for callers that cannot allocate (code under
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Limits: B*H/16 <= 512 and B*(H/16)*nsplit*32896 bytes of partials
+ * <= 16 MiB (nsplit after nsplit = 0 is resolved); a call beyond them returns
+ * DSA_ERR_UNSUPPORTED without launching.  Results equal (3)'s at the same
+ * nsplit, bit for bit.  Every call on a device shares that device's array:
+ * calls that overlap in time on one device (two streams, two threads) race
+ * and give wrong results.
+ * No counterpart in the reference (its launcher takes caller-owned scratch,
+ * P:1235-1241); added for callers that cannot allocate.
+ */
+int dsa_sparse_mla_decode_noalloc(const void* q_bf16, const void* kv_pool,
+                                  int64_t kv_rows, const int32_t* idx,
+                                  void* out_bf16, int B, int H, int topk,
+                                  int nsplit, float sm_scale, void* stream);
+
+/*
  * (4) One DSA decode layer on one stream:
  *   indexer scan -> top-k (position order, KV-slot output into next_idx),
  *   and attention over attend_idx (the lagged set: the attention and the
