@@ -102,6 +102,7 @@ int resolve_nsplit(int nsplit, int topk, int B, int H) {
 // recent earlier selection) instead of meaning "this layer's own selection".
 int check_layer(const dsa_layer_args* a, bool in_schedule = false) {
   DSA_REQUIRE(a != nullptr, DSA_ERR_INVALID_ARG, "dsa_layer_args is null");
+  DSA_REQUIRE(a->dense == 0 || a->dense == 1, DSA_ERR_INVALID_ARG, "dsa_layer_args.dense must be 0 or 1");
   int rc;
   if (a->q_fp8) {
     rc = check_scan(a->q_fp8, a->w, a->index_k, a->num_idx_pages, a->page_table, a->seq_lens,
@@ -111,7 +112,13 @@ int check_layer(const dsa_layer_args* a, bool in_schedule = false) {
                     a->next_idx, a->B, a->slab_stride, a->topk, DSA_TOPK_POSITION_ORDER);
     if (rc) return rc;
   }
-  if (a->q_bf16) {
+  if (a->q_bf16 && a->dense) {
+    DSA_REQUIRE(a->page_table && a->seq_lens && a->pt_stride >= 1, DSA_ERR_INVALID_ARG,
+                "dsa_decode_layer: dense attention needs page_table, pt_stride and seq_lens");
+    rc = check_mla(a->q_bf16, a->kv_pool, a->kv_rows, nullptr, a->workspace, a->out_bf16, a->B, a->H,
+                   a->pt_stride * DSA_PAGE_TOKENS, a->nsplit, /*idx_required=*/false);
+    if (rc) return rc;
+  } else if (a->q_bf16) {
     const int32_t* att = a->attend_idx ? a->attend_idx : a->next_idx;
     DSA_REQUIRE(in_schedule || a->attend_idx || a->q_fp8, DSA_ERR_INVALID_ARG,
                 "dsa_decode_layer: attention needs attend_idx or an indexer");
@@ -136,6 +143,19 @@ dsa::AttnArgs attn_args(const void* q_bf16, const void* kv_pool, int64_t kv_rows
   A.nsplit = resolve_nsplit(nsplit, topk, B, H);
   A.sm_log2 = sm_scale * 1.4426950408889634f;
   dsa::attn_bind_workspace(A, workspace, B);
+  return A;
+}
+
+// Dense attention over each row's first seq_lens[b] tokens (their KV slots
+// through the page table); the split count covers the page table's capacity.
+dsa::AttnArgs dense_attn_args(const void* q_bf16, const void* kv_pool, int64_t kv_rows,
+                              const int32_t* page_table, int pt_stride, const int32_t* seq_lens,
+                              void* workspace, void* out_bf16, int B, int H, int nsplit, float sm_scale) {
+  dsa::AttnArgs A = attn_args(q_bf16, kv_pool, kv_rows, nullptr, workspace, out_bf16, B, H,
+                              pt_stride * DSA_PAGE_TOKENS, nsplit, sm_scale);
+  A.dense_pt = page_table;
+  A.dense_lens = seq_lens;
+  A.dense_pt_stride = pt_stride;
   return A;
 }
 
@@ -174,18 +194,24 @@ int enqueue_layer(const dsa_layer_args* a, const int32_t* attend, bool with_inde
                   hipStream_t s) {
   dsa::AttnArgs A{};
   dsa::ScanArgs S{};
-  const bool attention = a->q_bf16 != nullptr && attend != nullptr;
-  const bool shared = attention && with_indexer && attend != a->next_idx;  // one launch, both roles
+  const bool dense = a->dense != 0;
+  const bool attention = a->q_bf16 != nullptr && (attend != nullptr || dense);
+  // one launch, both roles (the attention does not read this layer's selection)
+  const bool shared = attention && with_indexer && (dense || attend != a->next_idx);
+  const int att_keys = dense ? a->pt_stride * DSA_PAGE_TOKENS : a->topk;
+  const auto make_attn = [&](int nsplit) {
+    return dense ? dense_attn_args(a->q_bf16, a->kv_pool, a->kv_rows, a->page_table, a->pt_stride, a->seq_lens,
+                                   a->workspace, a->out_bf16, a->B, a->H, nsplit, a->sm_scale)
+                 : attn_args(a->q_bf16, a->kv_pool, a->kv_rows, attend, a->workspace, a->out_bf16, a->B, a->H,
+                             a->topk, nsplit, a->sm_scale);
+  };
   if (attention)
-    A = attn_args(a->q_bf16, a->kv_pool, a->kv_rows, attend, a->workspace, a->out_bf16, a->B,
-                  a->H, a->topk,
-                  a->nsplit > 0 ? a->nsplit : (shared ? dsa::attn_fused_nsplit(a->topk, a->B, a->H) : 0),
-                  a->sm_scale);
+    A = make_attn(a->nsplit > 0 ? a->nsplit : (shared ? dsa::attn_fused_nsplit(att_keys, a->B, a->H) : 0));
   if (with_indexer)
     S = scan_args(a->q_fp8, a->w, a->index_k, a->num_idx_pages, a->page_table, a->seq_lens,
                   a->scores, a->Hidx, a->pt_stride, a->slab_stride, a->topk_scratch, a->next_idx,
                   a->topk);
-  const bool own = attention && with_indexer && attend == a->next_idx;
+  const bool own = attention && with_indexer && !dense && attend == a->next_idx;
   int rc;
   if (with_indexer && a->B >= kSplitLaunchRows) {
     // large batches: a plain scan launch (two workgroups per CU) writes the
@@ -200,8 +226,7 @@ int enqueue_layer(const dsa_layer_args* a, const int32_t* attend, bool with_inde
     S.from_scores = 1;
     rc = hip_status(dsa::launch_decode_main(nullptr, 0, &S, a->B, s), "top-k select launch");
     if (rc || !attention) return rc;
-    if (a->nsplit <= 0) A = attn_args(a->q_bf16, a->kv_pool, a->kv_rows, attend, a->workspace, a->out_bf16,
-                                      a->B, a->H, a->topk, 0, a->sm_scale);
+    if (a->nsplit <= 0) A = make_attn(0);
     return hip_status(dsa::launch_decode_main(&A, a->B, nullptr, 0, s), "attention launch");
   }
   rc = hip_status(dsa::launch_decode_main(attention && !own ? &A : nullptr, a->B, with_indexer ? &S : nullptr,
@@ -235,7 +260,8 @@ int walk_mli(const dsa_layer_args* layers, int n, int depth, F&& on_layer) {
     const dsa_layer_args* a = &layers[i];
     const bool producer = a->q_fp8 != nullptr;
     const int32_t* lagged = (producer && depth >= 2 && produced >= depth) ? fresh[produced % depth] : carried;
-    const int32_t* att = a->attend_idx ? a->attend_idx : lagged;
+    // a dense layer attends no selection
+    const int32_t* att = a->dense ? nullptr : (a->attend_idx ? a->attend_idx : lagged);
     const int rc = on_layer(i, a, att);
     if (rc) return rc;
     carried = att;
@@ -256,7 +282,7 @@ int check_depth(int depth) {
 
 int enqueue_mli(const dsa_layer_args* layers, int n, int depth, hipStream_t s) {
   return walk_mli(layers, n, depth, [&](int i, const dsa_layer_args* a, const int32_t* att) {
-    if (a->q_bf16 && !att) return fail(DSA_ERR_INVALID_ARG, "mli layer %d: no selection to attend", i);
+    if (a->q_bf16 && !a->dense && !att) return fail(DSA_ERR_INVALID_ARG, "mli layer %d: no selection to attend", i);
     return enqueue_layer(a, a->q_bf16 ? att : nullptr, a->q_fp8 != nullptr, s);
   });
 }
@@ -268,7 +294,9 @@ int check_mli(const dsa_layer_args* layers, int n, int depth) {
   return walk_mli(layers, n, depth, [&](int i, const dsa_layer_args* a, const int32_t* att) {
     const int lrc = check_layer(a, true);
     if (lrc) return lrc;
-    if (a->q_bf16 && !att)
+    if (a->dense && depth != 1)
+      return fail(DSA_ERR_UNSUPPORTED, "mli layer %d: dense attention layers need lag depth 1", i);
+    if (a->q_bf16 && !a->dense && !att)
       return fail(DSA_ERR_INVALID_ARG, "mli layer %d: attend_idx is NULL and no earlier selection to attend", i);
     return DSA_OK;
   });
@@ -390,6 +418,22 @@ int dsa_sparse_mla_decode(const void* q_bf16, const void* kv_pool, int64_t kv_ro
                               nsplit, sm_scale);
   return hip_status(dsa::launch_decode_main(&A, B, nullptr, 0, (hipStream_t)stream),
                     "sparse MLA launch");
+}
+
+int dsa_dense_mla_decode(const void* q_bf16, const void* kv_pool, int64_t kv_rows,
+                         const int32_t* page_table, int pt_stride, const int32_t* seq_lens,
+                         void* workspace, void* out_bf16, int B, int H, int nsplit, float sm_scale,
+                         void* stream) {
+  DSA_REQUIRE(page_table && seq_lens && pt_stride >= 1, DSA_ERR_INVALID_ARG,
+              "dsa_dense_mla_decode: page_table, seq_lens and pt_stride >= 1 are required");
+  DSA_REQUIRE((int64_t)pt_stride * DSA_PAGE_TOKENS <= (int64_t)1 << 30, DSA_ERR_UNSUPPORTED,
+              "dsa_dense_mla_decode: pt_stride too large");
+  int rc = check_mla(q_bf16, kv_pool, kv_rows, nullptr, workspace, out_bf16, B, H, pt_stride * DSA_PAGE_TOKENS,
+                     nsplit, /*idx_required=*/false);
+  if (rc) return rc;
+  dsa::AttnArgs A = dense_attn_args(q_bf16, kv_pool, kv_rows, page_table, pt_stride, seq_lens, workspace,
+                                    out_bf16, B, H, nsplit, sm_scale);
+  return hip_status(dsa::launch_decode_main(&A, B, nullptr, 0, (hipStream_t)stream), "dense MLA launch");
 }
 
 int dsa_sparse_mla_decode_noalloc(const void* q_bf16, const void* kv_pool, int64_t kv_rows,

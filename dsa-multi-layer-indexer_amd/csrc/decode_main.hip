@@ -130,11 +130,20 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
   const uint32_t sense = (t == 0) ? group_sense(A.sync + ((long)b * nhg + hg) * kSyncWords, sp) : 0u;
   const int kps = (A.topk + nsplit - 1) / nsplit;
   const int k0 = min(A.topk, sp * kps), k1 = min(A.topk, k0 + kps);
+  // the KV slot of key j of the row: the selection's entry, or (dense) the
+  // slot of token j through the page table (-1 at or past the row's length)
   const int* idx_row = A.idx + (long)b * A.topk;
+  const int* dpt_row = A.dense_pt + (long)b * A.dense_pt_stride;
+  const int dlen = A.dense_pt ? max(0, min(A.dense_lens[b], A.topk)) : 0;
+  const auto key_slot = [&](int j) {
+    if (j >= k1) return -1;
+    if (!A.dense_pt) return idx_row[j];
+    return j < dlen ? dpt_row[j >> 6] * DSA_PAGE_TOKENS + (j & (DSA_PAGE_TOKENS - 1)) : -1;
+  };
 
   // the first two tiles' slots before the query (the gathers depend on them)
-  const int slot0 = (k0 + 16 * wv + kr < k1) ? idx_row[k0 + 16 * wv + kr] : -1;
-  int slot_next = (k0 + kTile + 16 * wv + kr < k1) ? idx_row[k0 + kTile + 16 * wv + kr] : -1;
+  const int slot0 = key_slot(k0 + 16 * wv + kr);
+  int slot_next = key_slot(k0 + kTile + 16 * wv + kr);
   // this lane's bytes of one key row (zeros for an invalid slot)
   struct RowRegs {
     uint4 nope[8], rope[2];
@@ -185,7 +194,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
     if (more) {
       load_row(slot_next, nxt);
       const int jn = tile0 + 2 * kTile + 16 * wv + kr;  // the slot after it, early
-      slot_next = (jn < k1) ? idx_row[jn] : -1;
+      slot_next = key_slot(jn);
     }
     const bool valid = cur.valid;
     const uint4* nope = cur.nope;

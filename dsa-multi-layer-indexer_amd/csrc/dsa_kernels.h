@@ -19,6 +19,12 @@ struct AttnArgs {
   uint16_t* out;         // [B, H, 512] bf16
   int H, topk, nsplit;
   float sm_log2;         // sm_scale * log2(e)
+  // dense attention (idx unused): key j of row b is token j, at KV slot
+  // dense_pt[b, j/64]*64 + j%64, for j < dense_lens[b]; topk = the keys a
+  // row may hold (dense_pt_stride * 64)
+  const int* dense_pt;   // [B, dense_pt_stride] or nullptr
+  const int* dense_lens; // [B]
+  int dense_pt_stride;
 };
 
 // Lightning-indexer scan over the paged fp8 index-K cache (scan role).

@@ -58,6 +58,7 @@ class LayerArgs(ctypes.Structure):
         ("B", _i32), ("Hidx", _i32), ("H", _i32), ("topk", _i32), ("nsplit", _i32),
         ("pt_stride", _i32), ("slab_stride", _i32),
         ("sm_scale", _f32),
+        ("dense", _i32),
     ]
 
 
@@ -73,6 +74,7 @@ SIGNATURES = {
     "dsa_topk": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
     "dsa_sparse_mla_workspace_bytes": (ctypes.c_size_t, [_i32, _i32, _i32]),
     "dsa_sparse_mla_decode": (_i32, [_vp, _vp, _i64, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _vp]),
+    "dsa_dense_mla_decode": (_i32, [_vp, _vp, _i64, _vp, _i32, _vp, _vp, _vp, _i32, _i32, _i32, _f32, _vp]),
     "dsa_sparse_mla_decode_noalloc": (_i32, [_vp, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _vp]),
     "dsa_decode_layer": (_i32, [ctypes.POINTER(LayerArgs), _vp]),
     "dsa_mli_graph_create": (_i32, [ctypes.POINTER(LayerArgs), _i32, _vp, ctypes.POINTER(_vp)]),

@@ -37,9 +37,6 @@ import torch
 from . import formats, ops
 from ._lib import INDEX_DIM, LATENT_DIM, PAGE_TOKENS, QK_DIM, TOPK_MAX_CTX
 
-_MAX_ATTEND = 16384  # keys one sparse-MLA row may attend (128 splits x 128)
-
-
 def _gpu(*ts: torch.Tensor) -> None:
     for t in ts:
         if not t.is_cuda:
@@ -75,13 +72,17 @@ def indexer_logits(index_q: torch.Tensor, index_k: torch.Tensor, weights: torch.
     dev = index_q.device
     Skv = index_k.shape[1]
     npg = max(1, (Skv + PAGE_TOKENS - 1) // PAGE_TOKENS)
-    # identity paging: batch b's page p is physical page b * npg + p
-    pages = formats.new_index_pool(B * npg, dev)
+    # identity paging: batch b's page p is physical page b * npg + p; every
+    # key of the batch quantized in one call and laid out page by page
     pt = (torch.arange(B, dtype=torch.int32, device=dev)[:, None] * npg
           + torch.arange(npg, dtype=torch.int32, device=dev)[None, :])
-    for b in range(B):
-        codes, sc = formats.quantize_rowwise(index_k[b])
-        formats.write_index_keys(pages, pt[b], codes, sc)
+    codes, sc = formats.quantize_rowwise(index_k.reshape(B * Skv, D))
+    kpad = torch.zeros(B, npg * PAGE_TOKENS, D, dtype=torch.uint8, device=dev)
+    kpad[:, :Skv] = codes.reshape(B, Skv, D)
+    spad = torch.zeros(B, npg * PAGE_TOKENS, dtype=torch.float32, device=dev)
+    spad[:, :Skv] = sc.reshape(B, Skv)
+    pages = torch.cat([kpad.reshape(B * npg, PAGE_TOKENS * D),
+                       spad.reshape(B * npg, PAGE_TOKENS).view(torch.uint8)], dim=1).contiguous()
     q8, wq = formats.quantize_index_query(index_q.reshape(B * S, H, D), weights.reshape(B * S, H))
     rows_pt = pt.repeat_interleave(S, dim=0).contiguous()
     seq = torch.full((B * S,), Skv, dtype=torch.int32, device=dev)
@@ -166,8 +167,6 @@ def sparse_mla_core(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tensor, va
     S, Skv = q.shape[1], kv.shape[1]
     if sm_scale is None:
         sm_scale = q.shape[-1] ** -0.5
-    if indices.shape[2] > _MAX_ATTEND:
-        raise ValueError(f"at most {_MAX_ATTEND} indices per row")
     idx = indices.long()
     q_pos = _q_pos(S, Skv, q.device)[None, :, None]
     ok = (idx >= 0) & (idx < Skv) & (idx <= q_pos)
@@ -176,19 +175,28 @@ def sparse_mla_core(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tensor, va
 
 def dense_mla_core(q: torch.Tensor, kv: torch.Tensor, value_dim: int,
                    sm_scale: float | None = None) -> torch.Tensor:
-    """Dense causal MLA (the layer-0 cold start, attention_core.py:142-160),
-    as sparse MLA over every causal key; S_kv <= 16384."""
+    """Dense causal MLA (full-attention layers and the DENSE cold start,
+    attention_core.py:142-160): query row s attends keys 0 .. S_kv - S + s,
+    on the dense MLA kernel (no limit on S_kv).  The latent rows are packed
+    to the fp8 format once, batch b's into pages of its own; every query row
+    is a decode row over its causal prefix of those pages."""
     _check_mla(q, kv, value_dim)
-    B, S = q.shape[0], q.shape[1]
+    B, S, H, _ = q.shape
     Skv = kv.shape[1]
-    if Skv > _MAX_ATTEND:
-        raise ValueError(f"dense attention here covers at most {_MAX_ATTEND} keys")
     if sm_scale is None:
         sm_scale = q.shape[-1] ** -0.5
-    k = torch.arange(Skv, device=q.device)[None, None, :].expand(B, S, Skv)
-    q_pos = _q_pos(S, Skv, q.device)[None, :, None]
-    idx = torch.where(k <= q_pos, k, torch.full_like(k, -1))
-    return _attend_rows(q, kv, idx, float(sm_scale))
+    dev = q.device
+    npg = max(1, (Skv + PAGE_TOKENS - 1) // PAGE_TOKENS)
+    rows = torch.zeros(B, npg * PAGE_TOKENS, QK_DIM, dtype=kv.dtype, device=dev)
+    rows[:, :Skv] = kv
+    pool = _pool_rows(rows)  # slot of (b, j) = b * npg * 64 + j
+    pt = (torch.arange(B, dtype=torch.int32, device=dev)[:, None] * npg
+          + torch.arange(npg, dtype=torch.int32, device=dev)[None, :])
+    pt_rows = pt.repeat_interleave(S, dim=0).contiguous()
+    lens = (_q_pos(S, Skv, dev) + 1).clamp(min=0).to(torch.int32).repeat(B).contiguous()
+    qb = q.reshape(B * S, H, QK_DIM).to(torch.bfloat16).contiguous()
+    out = ops.dense_mla_decode(qb, pool, pt_rows, lens, sm_scale=float(sm_scale))
+    return out.reshape(B, S, H, LATENT_DIM).to(q.dtype)
 
 
 _NAMES = ("pad_index", "indexer_logits", "apply_causal_mask", "select_topk", "sparse_mla_core",

@@ -42,6 +42,7 @@ class DecodeLayer:
     topk: int = 2048
     nsplit: int = 0
     sm_scale: float = 576 ** -0.5
+    dense: bool = False               # attention over the whole prefix (full layer / DENSE cold start)
 
     def __post_init__(self) -> None:
         B = self.q_bf16.shape[0]
@@ -86,11 +87,13 @@ class DecodeLayer:
         a.pt_stride = self.page_table.shape[1]
         a.slab_stride = self.slab_stride
         a.sm_scale = self.sm_scale
+        a.dense = 1 if (self.dense and attention) else 0
         return a
 
     def run(self, attend_idx: torch.Tensor | None = None) -> None:
         """One layer on the current stream: indexer -> next_idx, attention
-        over attend_idx (lagged) or over next_idx (same-layer, baseline DSA)."""
+        over attend_idx (lagged) or over next_idx (same-layer, baseline DSA),
+        or over the whole prefix when the layer is dense."""
         a = self.args(attend_idx)
         _lib.call("dsa_decode_layer", ctypes.byref(a), torch.cuda.current_stream().cuda_stream)
 

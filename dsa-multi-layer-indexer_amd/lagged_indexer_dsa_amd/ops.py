@@ -170,6 +170,41 @@ def sparse_mla_decode(q: torch.Tensor, kv_pool: torch.Tensor, idx: torch.Tensor,
     return out
 
 
+def dense_mla_decode(q: torch.Tensor, kv_pool: torch.Tensor, page_table: torch.Tensor, seq_lens: torch.Tensor,
+                     sm_scale: float | None = None, nsplit: int = 0,
+                     workspace: torch.Tensor | None = None,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """Dense MLA of each decode row over its first seq_lens[b] tokens, their
+    latent rows found through the page table (64-token pages).
+
+    q [B,H,576] bf16; kv_pool [rows,656] uint8; page_table [B,pt] int32;
+    seq_lens [B] int32  ->  out [B,H,512] bf16.
+    Reference: attention_core.py:142-160 dense_mla_core; model.py:104-114.
+    """
+    _dev(q, kv_pool, page_table, seq_lens)
+    if q.dim() != 3 or q.shape[2] != QK_DIM or q.dtype != torch.bfloat16:
+        raise RuntimeError("q must be [B, H, 576] bfloat16")
+    B, H, _ = q.shape
+    if kv_pool.dim() != 2 or kv_pool.shape[1] != LATENT_ROW_BYTES or kv_pool.dtype != torch.uint8:
+        raise RuntimeError("kv_pool must be [rows, 656] uint8")
+    if page_table.dim() != 2 or page_table.shape[0] != B or page_table.dtype != torch.int32:
+        raise RuntimeError("page_table must be [B, pt_stride] int32")
+    _need_shape("seq_lens", seq_lens, (B,), torch.int32)
+    if sm_scale is None:
+        sm_scale = QK_DIM ** -0.5
+    if workspace is None:
+        workspace = sparse_mla_workspace(B, H, nsplit, q.device)
+    if out is None:
+        out = torch.empty(B, H, LATENT_DIM, dtype=torch.bfloat16, device=q.device)
+    _dev(workspace, out)
+    _need_shape("out", out, (B, H, LATENT_DIM), torch.bfloat16)
+    _need_bytes("sparse MLA workspace", workspace, _lib.load().dsa_sparse_mla_workspace_bytes(B, H, nsplit))
+    _lib.call("dsa_dense_mla_decode", q.data_ptr(), kv_pool.data_ptr(), kv_pool.shape[0], page_table.data_ptr(),
+              page_table.shape[1], seq_lens.data_ptr(), workspace.data_ptr(), out.data_ptr(), B, H, nsplit,
+              float(sm_scale), _stream())
+    return out
+
+
 # ---- decode-step operand preparation (the inputs the decode layer reads) ----
 
 def quantize_index_query(q: torch.Tensor, w: torch.Tensor, out_q: torch.Tensor | None = None,

@@ -165,6 +165,21 @@ int dsa_sparse_mla_decode(const void* q_bf16, const void* kv_pool,
                           float sm_scale, void* stream);
 
 /*
+ * (3a) Dense MLA decode: the attention of (3) over every token of each row,
+ * keys 0..seq_lens[b]-1 at KV slots page_table[b*pt_stride + j/64]*64 + j%64
+ * (seq_lens clamped to pt_stride*64).  workspace:
+ * dsa_sparse_mla_workspace_bytes(B, H, nsplit), as for (3); nsplit = 0:
+ * one split per 64 keys of the page table's capacity, at most 128.
+ * Replaces: dense_mla_core (attention_core.py:142-160), the full-attention
+ * layers and the DENSE cold start of DSAModel.forward (model.py:51-59,
+ * 104-114).
+ */
+int dsa_dense_mla_decode(const void* q_bf16, const void* kv_pool, int64_t kv_rows,
+                         const int32_t* page_table, int pt_stride, const int32_t* seq_lens,
+                         void* workspace, void* out_bf16, int B, int H, int nsplit,
+                         float sm_scale, void* stream);
+
+/*
  * (3b) The same sparse MLA decode with no workspace argument and no
  * allocation: the split partials and the per-(row, head group) barriers live
  * in a static device array of the library (one copy per device, about 19 MB,
@@ -217,6 +232,10 @@ typedef struct dsa_layer_args {
   const int32_t* seq_lens;  /* [B] */
   int B, Hidx, H, topk, nsplit, pt_stride, slab_stride;
   float sm_scale;
+  /* 1: the attention is dense over each row's first seq_lens[b] tokens
+   * (attend_idx ignored) -- a full-attention layer, or the DENSE cold start
+   * of layer 0; 0: sparse over attend_idx / the schedule's selection */
+  int dense;
 } dsa_layer_args;
 /* nsplit = 0: automatic.  The attention launched alone takes one split per
  * 64 selected keys, at most one workgroup per CU over the batch's (row, head
@@ -231,7 +250,8 @@ int dsa_decode_layer(const dsa_layer_args* args, void* stream);
 /*
  * (5) MLI lag schedule over a stack of layers, eagerly or as one hipGraph.
  * Layer i attends the selection of the most recent earlier layer that runs
- * an indexer (its attend_idx when given; layer 0 must be given one), and
+ * an indexer (its attend_idx when given; layer 0 must be given one, unless
+ * it is dense), or densely when its `dense` flag is set, and
  * layer i's indexer scan runs in the SAME launch as layer i's attention
  * (role-decoupled workgroups; from B = 8 rows scan, select and attention
  * are three launches), followed by layer i's
