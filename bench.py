@@ -17,8 +17,10 @@ region -- the fused layer launch, timed with HIP events per replay on the
 stream it is launched on -- and the CPU baseline (the reference's fp32
 decode-row path restated in oracle/, timed on this host).
 
---profile-main runs only a calibration copy of known size and the timed
-region (for rocprofv3 kernel-trace and counter runs).
+--profile ROLE runs only a calibration read of known size (the library's
+speed-of-light read kernel) and one kind of launch -- the fused layer graph
+(the timed region), or the scan, top-k or attention launches alone -- for
+rocprofv3 kernel-trace and counter runs (--profile-main = --profile fused).
 """
 
 from __future__ import annotations
@@ -37,7 +39,6 @@ sys.path.insert(0, str(REPO))
 
 HBM_PEAK_GBS = 8000.0
 MALL_DEFEAT_BYTES = 768 << 20  # 3x the 256 MB Infinity Cache
-COPY_BYTES = 256 << 20  # calibration copy for the byte counters (read = write = this)
 TRAFFIC_FILE = REPO / "profiles" / "decode_layer_c3_hbm_traffic.md"
 CONFIGS = {
     "c2": dict(lens=[32768], layers=2, indexer_every=1, desc="v32_ctx32768_b1_2layer_mli_graph"),
@@ -109,6 +110,36 @@ def graph_event_ms(fn, iters: int, torch) -> float:
     return a.elapsed_time(b) / iters
 
 
+def speed_of_light(lib, nbytes: int, torch, launches: int = 96) -> dict:
+    """What one launch can reach on this part, timed like the scan (graph of
+    back-to-back launches, HIP events): an empty launch, and a pure
+    dependency-free read of `nbytes` per launch rotating over enough buffers
+    (>= 768 MB) that every launch streams from HBM."""
+    import ctypes
+
+    dev = torch.device("cuda:0")
+    nbuf = max(2, -(-MALL_DEFEAT_BYTES // nbytes))
+    bufs = [torch.ones(nbytes // 4, dtype=torch.int32, device=dev) for _ in range(nbuf)]
+    sink = torch.zeros(16, dtype=torch.int32, device=dev)
+    lib.dsa_internal_sol_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
+                                          ctypes.c_void_p]
+    lib.dsa_internal_sol_empty.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    st = {"i": 0}
+
+    def read():
+        lib.dsa_internal_sol_read(bufs[st["i"] % nbuf].data_ptr(), nbytes, sink.data_ptr(), 512,
+                                  torch.cuda.current_stream().cuda_stream)
+        st["i"] += 1
+
+    def empty():
+        lib.dsa_internal_sol_empty(sink.data_ptr(), 512, torch.cuda.current_stream().cuda_stream)
+    read_ms = graph_event_ms(read, launches, torch)
+    empty_ms = graph_event_ms(empty, launches, torch)
+    del bufs
+    return {"empty_launch_us": round(empty_ms * 1e3, 3), "read_us": round(read_ms * 1e3, 3),
+            "read_bytes": nbytes, "read_GBps": round(nbytes / (read_ms * 1e-3) / 1e9, 1)}
+
+
 def read_traffic():
     """HBM bytes per fused layer launch measured by the rocprofv3 counter runs
     (FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy) recorded in
@@ -157,12 +188,15 @@ def main() -> int:
                     help="attention splits per (row, head group); 0 = the library's choice")
     ap.add_argument("--max-sets", type=int, default=64,
                     help="cap on the rotated layer sets (1: no Infinity-Cache defeat)")
-    ap.add_argument("--profile-main", action="store_true",
-                    help="only the calibration copy and the timed region (profiler runs)")
+    ap.add_argument("--profile", choices=["fused", "scan", "topk", "attn"], default=None,
+                    help="only the calibration read and one kind of launch (profiler runs)")
+    ap.add_argument("--profile-main", action="store_true", help="= --profile fused")
     ap.add_argument("--graph-packet-capture", action="store_true",
                     help="keep the HIP runtime's default graph launch mode (captured AQL packets), "
                          "which adds ~3.5 us to every replay")
     args = ap.parse_args()
+    if args.profile_main:
+        args.profile = "fused"
     # The HIP runtime replays a graph either from AQL packets it captured at
     # instantiation (its default) or by launching the graph's nodes on the
     # stream.  On this stack the first costs ~4.7 us per replay more than
@@ -226,14 +260,38 @@ def main() -> int:
             state["i"] += 1
         return fn
 
-    if args.profile_main:
-        # calibration for the HBM byte counters: a plain copy of known size
-        src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+    L0s = [ls[0] for ls in sets]
+
+    def rot_layers(make):
+        fns = [make(L) for L in L0s]
+        state = {"i": 0}
+
+        def fn():
+            fns[state["i"] % len(fns)]()
+            state["i"] += 1
+        return fn
+    scan = rot_layers(lambda L: lambda: ops.indexer_scan(L.q_fp8, L.w, L.index_k, L.page_table,
+                                                         L.seq_lens, L.slab_stride, out=L.scores))
+    topk_fn = rot_layers(lambda L: lambda: ops.topk(L.scores, L.seq_lens, 2048, page_table=L.page_table,
+                                                    out=L.next_idx, scratch=L.topk_scratch))
+    attn_fn = rot_layers(lambda L: lambda: ops.sparse_mla_decode(L.q_bf16, L.kv_pool, first, nsplit=L.nsplit,
+                                                                 workspace=L.workspace, out=L.out))
+
+    if args.profile:
+        # calibration for the HBM byte counters: the speed-of-light read
+        # kernel over buffers of the scan's size (its bytes are known)
+        sol = speed_of_light(_lib.load(), scan_bytes(lens), torch, launches=20)
+        if args.profile != "fused":
+            fn = {"scan": scan, "topk": topk_fn, "attn": attn_fn}[args.profile]
+            for _ in range(args.warmup):
+                fn()
+            torch.cuda.synchronize()
+            ms = graph_event_ms(fn, max(20, args.steps), torch)
+            for s in scheds:
+                s.close()
+            print(json.dumps({"profile": args.profile, "sets": n_sets, "launch_us": round(ms * 1e3, 3),
+                              "calibration": sol}), flush=True)
+            return 0
 
     _lib.sync_timeouts(reset=True)
     for i in range(args.warmup):
@@ -263,12 +321,12 @@ def main() -> int:
     # per launch, averaged over the step's layers (IndexCache layers run no scan)
     n_idx = sum(1 for i in range(n_layers) if i % cfg["indexer_every"] == 0)
     lb = (n_idx * scan_bytes(lens) + n_layers * attn_bytes(B)) // n_layers
-    if args.profile_main:
+    if args.profile:
         for s in scheds:
             s.close()
-        print(json.dumps({"profile_main": True, "sets": n_sets, "us_per_layer": round(ms_step * 1e3 / n_layers, 3),
+        print(json.dumps({"profile": "fused", "sets": n_sets, "us_per_layer": round(ms_step * 1e3 / n_layers, 3),
                           "launch_us": round(launch_ms * 1e3, 3), "layer_bytes": lb,
-                          "copy_bytes": COPY_BYTES}), flush=True)
+                          "calibration": sol}), flush=True)
         return 0
 
     reps = max(20, args.steps // 2)
@@ -289,18 +347,6 @@ def main() -> int:
 
     # ---- the standalone ops (scan-only launches, the top-k (position order: one select launch), the
     # attention alone), each rotating over the sets' first layers ----
-    L0s = [ls[0] for ls in sets]
-
-    def rot_layers(make):
-        fns = [make(L) for L in L0s]
-        state = {"i": 0}
-
-        def fn():
-            fns[state["i"] % len(fns)]()
-            state["i"] += 1
-        return fn
-    scan = rot_layers(lambda L: lambda: ops.indexer_scan(L.q_fp8, L.w, L.index_k, L.page_table,
-                                                         L.seq_lens, L.slab_stride, out=L.scores))
     for _ in range(10):
         scan()
     n_graph = max(50, 2 * n_sets)
@@ -308,11 +354,7 @@ def main() -> int:
     scan_ms_pairs = event_ms(scan, 100, torch)
     sb = scan_bytes(lens)
     scan_gbs = sb / (scan_ms * 1e-3) / 1e9
-    topk_fn = rot_layers(lambda L: lambda: ops.topk(L.scores, L.seq_lens, 2048, page_table=L.page_table,
-                                                    out=L.next_idx, scratch=L.topk_scratch))
     topk_ms = graph_event_ms(topk_fn, n_graph, torch)
-    attn_fn = rot_layers(lambda L: lambda: ops.sparse_mla_decode(L.q_bf16, L.kv_pool, first, nsplit=L.nsplit,
-                                                                 workspace=L.workspace, out=L.out))
     attn_ms = graph_event_ms(attn_fn, n_graph, torch)
     ab = attn_bytes(B)
     # decode-step operand preparation for one layer: quantize the indexer
@@ -337,6 +379,7 @@ def main() -> int:
         ops.append_latent_rows(Lp.kv_pool, slot_i, new_lat)
     prep_ms = graph_event_ms(prep, 50, torch)
 
+    sol = speed_of_light(_lib.load(), sb, torch)
     us_layer = ms_step * 1e3 / n_layers
     layer_gbs = lb / (launch_ms * 1e-3) / 1e9
     res = {
@@ -368,6 +411,8 @@ def main() -> int:
                       "sparse_mla+combine": round(attn_ms * 1e3, 3),
                       "indexer_scan_event_pairs": round(scan_ms_pairs * 1e3, 3)},
         "attention_gather_GBps": round(ab / (attn_ms * 1e-3) / 1e9, 1),
+        # the scan against what one launch of its bytes can reach here
+        "speed_of_light": dict(sol, indexer_scan_frac=round(sol["read_us"] / (scan_ms * 1e3), 4)),
         "mli": {"graph_ms": round(t_full, 5), "eager_ms": round(t_eager, 5),
                 "serial_ms": round(t_attn + t_idx, 5),
                 "eager_layer_calls_ms": round(t_serial, 5), "attn_only_ms": round(t_attn, 5),

@@ -433,6 +433,7 @@ __device__ __forceinline__ uint32_t union_slot(uint32_t b) { return b + (b / kUn
 constexpr int kCoarseOff = kHistBins + 64;
 constexpr int kCoarseSpillOff = kCoarseOff + 64;
 constexpr int kHistWords = kCoarseSpillOff + 32;
+static_assert(kUnionWords + kWave <= kHistWords, "the union histogram and its per-lane spill words fit the histogram area");
 struct ScanShared {
   uint8_t qs[64 * DSA_INDEX_DIM];
   float ws[64];
@@ -943,12 +944,17 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
     uint32_t T1 = 0, above = 0, nbin = 0;
     int sh = 0;
     if (ok) {
-      // the bit window that spreads [lo, hi] over <= kUnionBins bins
-      while (sh < 32 && (hi >> sh) - (lo >> sh) >= (uint32_t)kUnionBins) ++sh;
+      // a bit window that spreads [lo, hi] over <= 1025 of the kUnionBins
+      // bins: (hi - lo) >> sh < 1024, so (hi >> sh) - (lo >> sh) <= 1024
+      {
+        const uint32_t d = hi - lo;
+        sh = d < 1024u ? 0 : 32 - __builtin_clz(d) - 10;
+      }
       const uint32_t base = lo >> sh;
       uint32_t* hist = cs.scan.hist;
       // branch-free: keys below lo land in spill bins past the histogram
-      const uint32_t spill = kUnionWords + (t & 31);
+      // (a spill word per lane: the lanes' atomics never collide)
+      const uint32_t spill = kUnionWords + (uint32_t)(t & (kWave - 1));
       for_mine([&](uint32_t w, uint32_t) { atomicAdd(&hist[w >= lo ? union_slot((w >> sh) - base) : spill], 1u); });
       __syncthreads();
       dbg_stamp(dbk, 12);
@@ -1514,6 +1520,7 @@ __global__ __launch_bounds__(kMainThreads, (ROLES & ~kRolePlan) == kRoleScan ? 4
                                                                                              ScanArgs S) {
   extern __shared__ __align__(16) unsigned char smem[];
   int bid = blockIdx.x;
+  dbg_begin();
   if constexpr ((ROLES & kRoleAttn) != 0) {
     if (bid < n_att) {
       const int nhg = A.H / kHG;
@@ -1521,6 +1528,7 @@ __global__ __launch_bounds__(kMainThreads, (ROLES & ~kRolePlan) == kRoleScan ? 4
       const int hg = (bid / A.nsplit) % nhg;
       const int b = bid / (A.nsplit * nhg);
       attention_block(A, b, hg, sp, smem);
+      dbg_flush(blockIdx.x);
       return;
     }
   }
@@ -1537,6 +1545,7 @@ __global__ __launch_bounds__(kMainThreads, (ROLES & ~kRolePlan) == kRoleScan ? 4
     }
     scan_block<NHG, VARIANT, (ROLES & kRoleSelect) != 0, (ROLES & kRoleFromScores) != 0, (ROLES & kRoleTopk) != 0>(
         S, row, bid, nb, smem);
+    dbg_flush(blockIdx.x);
   }
 }
 

@@ -337,23 +337,34 @@ constexpr int kDbgPhases = 16;
 extern __device__ int g_dbg_on;
 extern __device__ unsigned long long g_dbg[kDbgBlocks * kDbgPhases];
 #ifdef DSA_PHASE_STAMPS
-// (profiling builds record unconditionally: a store does not wait)
+// Profiling builds record into LDS (no memory traffic, so a stamp does not
+// delay the launch's own waits for its loads and stores) and copy the
+// workgroup's stamps to g_dbg once, at its end (dbg_flush).
 constexpr bool kPhaseStamps = true;
-__device__ __forceinline__ void dbg_stamp(int blk, int ph) {
-  if (threadIdx.x == 0 && blk < kDbgBlocks) g_dbg[blk * kDbgPhases + ph] = __builtin_amdgcn_s_memrealtime();
+__shared__ unsigned long long s_dbg_marks[kDbgPhases];
+__device__ __forceinline__ void dbg_begin() {
+  if (threadIdx.x < kDbgPhases) s_dbg_marks[threadIdx.x] = 0ull;
 }
-
+__device__ __forceinline__ void dbg_stamp(int, int ph) {
+  if (threadIdx.x == 0) s_dbg_marks[ph] = __builtin_amdgcn_s_memrealtime();
+}
 // Same, recorded by lane 0 of wave `w` instead of thread 0.
-__device__ __forceinline__ void dbg_stamp_wave(int blk, int ph, int w) {
-  if (threadIdx.x == (unsigned)(w * kWave) && blk < kDbgBlocks)
-    g_dbg[blk * kDbgPhases + ph] = __builtin_amdgcn_s_memrealtime();
+__device__ __forceinline__ void dbg_stamp_wave(int, int ph, int w) {
+  if (threadIdx.x == (unsigned)(w * kWave)) s_dbg_marks[ph] = __builtin_amdgcn_s_memrealtime();
 }
 // a value instead of a time (the probe reads it from the same table)
-__device__ __forceinline__ void dbg_value(int blk, int ph, unsigned long long v) {
-  if (threadIdx.x == 0 && blk < kDbgBlocks) g_dbg[blk * kDbgPhases + ph] = v;
+__device__ __forceinline__ void dbg_value(int, int ph, unsigned long long v) {
+  if (threadIdx.x == 0) s_dbg_marks[ph] = v;
+}
+// every thread of the workgroup calls it once, at the end
+__device__ __forceinline__ void dbg_flush(int blk) {
+  __syncthreads();
+  if (threadIdx.x < kDbgPhases && blk < kDbgBlocks) g_dbg[blk * kDbgPhases + threadIdx.x] = s_dbg_marks[threadIdx.x];
 }
 #else
 constexpr bool kPhaseStamps = false;
+__device__ __forceinline__ void dbg_begin() {}
+__device__ __forceinline__ void dbg_flush(int) {}
 __device__ __forceinline__ void dbg_value(int, int, unsigned long long) {}
 __device__ __forceinline__ void dbg_stamp(int, int) {}
 __device__ __forceinline__ void dbg_stamp_wave(int, int, int) {}

@@ -6,3 +6,4 @@
 #include "decode_main.hip"
 #include "quant.hip"
 #include "capi.hip"
+#include "sol.hip"
