@@ -188,7 +188,7 @@ def main() -> int:
                     help="attention splits per (row, head group); 0 = the library's choice")
     ap.add_argument("--max-sets", type=int, default=64,
                     help="cap on the rotated layer sets (1: no Infinity-Cache defeat)")
-    ap.add_argument("--profile", choices=["fused", "scan", "topk", "attn"], default=None,
+    ap.add_argument("--profile", choices=["fused", "scan", "topk", "attn", "two_stream"], default=None,
                     help="only the calibration read and one kind of launch (profiler runs)")
     ap.add_argument("--profile-main", action="store_true", help="= --profile fused")
     ap.add_argument("--graph-packet-capture", action="store_true",
@@ -281,6 +281,63 @@ def main() -> int:
         # calibration for the HBM byte counters: the speed-of-light read
         # kernel over buffers of the scan's size (its bytes are known)
         sol = speed_of_light(_lib.load(), scan_bytes(lens), torch, launches=20)
+        if args.profile == "two_stream":
+            # the second-stream design: attention launches on one stream,
+            # scan launches on another, no ordering between the two; the
+            # kernel trace shows whether their executions overlap
+            sa, sb2 = torch.cuda.Stream(), torch.cuda.Stream()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(max(20, args.steps)):
+                with torch.cuda.stream(sa):
+                    attn_fn()
+                with torch.cuda.stream(sb2):
+                    scan()
+            torch.cuda.synchronize()
+            ms = (time.perf_counter() - t0) * 1e3 / max(20, args.steps)
+
+            # the same pair as graphs (no host launch cost): two branches
+            # forked from one stream and joined, against one stream
+            def pair_graph(two: bool):
+                g = torch.cuda.CUDAGraph()
+                cap = torch.cuda.Stream()
+                cap.wait_stream(torch.cuda.current_stream())
+                with torch.cuda.stream(cap):
+                    with torch.cuda.graph(g, stream=cap):
+                        for _ in range(20):
+                            if two:
+                                sa.wait_stream(cap)
+                                sb2.wait_stream(cap)
+                                with torch.cuda.stream(sa):
+                                    attn_fn()
+                                with torch.cuda.stream(sb2):
+                                    scan()
+                                cap.wait_stream(sa)
+                                cap.wait_stream(sb2)
+                            else:
+                                attn_fn()
+                                scan()
+                torch.cuda.current_stream().wait_stream(cap)
+                return g
+
+            def replay_ms(g):
+                g.replay()
+                torch.cuda.synchronize()
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                for _ in range(5):
+                    g.replay()
+                b.record()
+                torch.cuda.synchronize()
+                return a.elapsed_time(b) / (5 * 20)
+            g2, g1 = pair_graph(True), pair_graph(False)
+            two_ms, one_ms = replay_ms(g2), replay_ms(g1)
+            for s in scheds:
+                s.close()
+            print(json.dumps({"profile": "two_stream", "eager_ms_per_pair": round(ms, 5),
+                              "graph_two_branches_ms_per_pair": round(two_ms, 5),
+                              "graph_one_stream_ms_per_pair": round(one_ms, 5)}), flush=True)
+            return 0
         if args.profile != "fused":
             fn = {"scan": scan, "topk": topk_fn, "attn": attn_fn}[args.profile]
             for _ in range(args.warmup):
