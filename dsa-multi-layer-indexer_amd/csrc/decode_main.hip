@@ -317,21 +317,24 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
   const int g = t / span;
   constexpr int kLd = 8;                   // partial loads in flight per thread
   float4 x[kLd];
+  // every load is issued (an unused one reads past the resource: 0), so
+  // the compiler can wait for each batch by count
   auto load_x = [&](int v, int s0, int s1) {
 #pragma unroll
     for (int i = 0; i < kLd; ++i)
-      x[i] = (s0 + i < s1) ? __builtin_bit_cast(float4, load_dev16(prs, 16u * ((s0 + i) * kVec + v)))
-                           : make_float4(0.f, 0.f, 0.f, 0.f);
+      x[i] = __builtin_bit_cast(float4, load_dev16(prs, s0 + i < s1 ? 16u * ((s0 + i) * kVec + v) : 0xfffffff0u));
   };
-  if (g < G && t - g * span < nv) load_x(v_lo + t - g * span, g * spg, min(nsplit, (g + 1) * spg));
-  {  // nsplit*32 floats, <= 8 per thread
+  {  // the splits' (m, l) first (nsplit*32 floats, <= 8 per thread), then this
+     // thread's partials: the merge weights are computed while those arrive
     constexpr int kPer = kMaxSplit * 2 * kHG / kMainThreads;
     float v[kPer];
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
       const int i = t + j * kMainThreads;
-      v[j] = (i < nsplit * 2 * kHG) ? __uint_as_float(load_dev4(mrs, 4u * i)) : 0.f;
+      v[j] = __uint_as_float(load_dev4(mrs, i < nsplit * 2 * kHG ? 4u * i : 0xfffffffcu));
     }
+    const bool act = g < G && t - g * span < nv;
+    load_x(v_lo + t - g * span, act ? g * spg : 0, act ? min(nsplit, (g + 1) * spg) : 0);
 #pragma unroll
     for (int j = 0; j < kPer; ++j)
       if (t + j * kMainThreads < nsplit * 2 * kHG) mls[t + j * kMainThreads] = v[j];
@@ -768,7 +771,10 @@ __device__ __forceinline__ uint32_t lane_rank(uint64_t m) {
 // fine and coarse histograms, and cs.wstat.
 // pts: this workgroup's page-table entries from page pg0 on (in LDS) when
 // pts_lds, else the row's page table is read from memory.
-template <bool TOPK>
+// NU: uint4s of the union each thread holds (thread t: t, t + 512, ...);
+// past the union they read as 0, below every bound, so every per-entry loop
+// runs NU times without a guard.
+template <bool TOPK, int NU>
 __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem, const ScanArgs& S, int bid,
                                             int nb, int len, int p_lo, int p_hi, uint32_t* rs,
                                             const float* srow, const int* pt_row, int* o, const int* pts,
@@ -874,8 +880,8 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
   // device-scope loads; thread t holds uint4s t, t + 512, ... of the area)
   // and the headers' reductions ----
   const int nent = all ? 0 : nb * P;
-  const int n4 = nent >> 2;
-  constexpr int kU = kPubWords / 4 / kMainThreads;
+  constexpr int kU = NU;
+  static_assert(NU * 4 * kMainThreads <= kPubWords, "union registers");
   uint4 u[kU];
   {
     uint32_t hdr_b = 0, hdr_f = 0, hdr_m = 0;
@@ -889,7 +895,7 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
 #pragma unroll
     for (int j = 0; j < kU; ++j) {
       const int i = t + j * kMainThreads;
-      u[j] = (j * kMainThreads < n4) ? load_dev16(r, 16u * i) : make_uint4(0, 0, 0, 0);  // 0 past the end
+      u[j] = load_dev16(r, 16u * i);  // 0 past the end of the resource
     }
     for (int i = t; i < kUnionWords; i += kMainThreads) cs.scan.hist[i] = 0u;
     if (t < kWave) cs.ck[t] = 0u;  // candidates past the count read as 0
@@ -917,7 +923,6 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
   const auto for_mine = [&](auto&& f) {
 #pragma unroll
     for (int j = 0; j < kU; ++j) {
-      if (j * kMainThreads >= n4) break;  // uniform
       const uint32_t e = 4u * (uint32_t)(t + j * kMainThreads);
       f(u[j].x, e);
       f(u[j].y, e + 1u);
@@ -980,7 +985,6 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
     uint32_t ax = 0, az = 0, cmask = 0;
 #pragma unroll
     for (int j = 0; j < kU; ++j) {
-      if (j * kMainThreads >= n4) break;  // uniform
       const bool before = 4u * (uint32_t)(t + j * kMainThreads) < mine0;
       const uint32_t w4[4] = {u[j].x, u[j].y, u[j].z, u[j].w};
       uint32_t gj = 0;
@@ -1440,9 +1444,17 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   if constexpr (!SELECT) return;
   if (!S.next_idx) return;
   if (S.coop) {
-    coop_select<TOPK>(*reinterpret_cast<CoopShared*>(smem), smem, S, bid, nb, len, c0 * kChunkKeys,
-                min(c1 * kChunkKeys, len), rs, srow, pt_row, S.next_idx + (long)row * S.topk, sh.pts, pg0,
-                pts_lds);
+    // the union's uint4s per thread: 4 (up to 8192 entries, C3's 224 lists)
+    // or 8, each its own instantiation
+    CoopShared& cs = *reinterpret_cast<CoopShared*>(smem);
+    int* o = S.next_idx + (long)row * S.topk;
+    const int p_hi = min(c1 * kChunkKeys, len);
+    if (nb * pub_stride(nb, S.topk) <= 4 * 4 * kMainThreads)
+      coop_select<TOPK, 4>(cs, smem, S, bid, nb, len, c0 * kChunkKeys, p_hi, rs, srow, pt_row, o, sh.pts, pg0,
+                           pts_lds);
+    else
+      coop_select<TOPK, 8>(cs, smem, S, bid, nb, len, c0 * kChunkKeys, p_hi, rs, srow, pt_row, o, sh.pts, pg0,
+                           pts_lds);
     return;
   }
   // arrival: wait for this slice's device-scope score stores and histogram
