@@ -436,11 +436,12 @@ __device__ __forceinline__ uint32_t union_slot(uint32_t b) { return b + (b / kUn
 constexpr int kCoarseOff = kHistBins + 64;
 constexpr int kCoarseSpillOff = kCoarseOff + 64;
 constexpr int kHistWords = kCoarseSpillOff + 32;
+static_assert(kHistWords % 4 == 0, "the histogram area is cleared in uint4s");
 static_assert(kUnionWords + kWave <= kHistWords, "the union histogram and its per-lane spill words fit the histogram area");
 struct ScanShared {
   uint8_t qs[64 * DSA_INDEX_DIM];
   float ws[64];
-  uint32_t hist[kHistWords];
+  alignas(16) uint32_t hist[kHistWords];
   int pts[kScanMaxPages];
 };
 
@@ -482,10 +483,10 @@ static_assert(kCoopKeys <= 65536, "own positions are stored as 16-bit indices");
 // barrier, so capacity costs load time.
 // A list too short for its workgroup only costs the fallback to the
 // histogram form.
-__host__ __device__ inline int pub_target(int nb, int K) { return 2 * ((K + nb - 1) / nb) + 8; }
+__host__ __device__ inline int pub_target(int nb, int K) { return 2 * (int)(((uint32_t)K + nb - 1) / (uint32_t)nb) + 8; }
 __host__ __device__ inline int pub_stride(int nb, int K) {
-  const int want = pub_target(nb, K) + ((K + nb - 1) / nb + 1) / 2;
-  return min((want + 3) & ~3, (kPubWords / nb) & ~3);
+  const int want = pub_target(nb, K) + (int)((((uint32_t)K + nb - 1) / (uint32_t)nb + 1) / 2);
+  return min((want + 3) & ~3, (int)((uint32_t)kPubWords / (uint32_t)nb) & ~3);
 }
 
 // Histogram form of the cooperative select (the general case; the
@@ -840,6 +841,8 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
     }
   }
 
+  dbg_stamp(dbk, 25);
+  dbg_value(dbk, 27, all ? 9ull : ((uint32_t)nown <= (uint32_t)P ? 3ull : (lo_b == 0u ? 4ull : ((lo_b & 0xfffffu) ? 2ull : 0ull))));
   // ---- publish in position order: thread t takes contiguous positions and
   // one block scan gives it its slots; the entries' positions stay in LDS
   // (lpos, shared with the histogram form's candidates, which that form
@@ -856,6 +859,7 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
       uint32_t tot;
       // no closing barrier: wave_tmp is next written after the group barrier
       uint32_t off = block_exclusive_scan<false>(c, cs.wave_tmp, &tot);  // tot == cnt
+      dbg_stamp(dbk, 26);
       for (int i = i0; i < i1; ++i) {
         const uint32_t k = cs.keys[i];
         if (k >= lo_b) {
@@ -949,23 +953,24 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
     uint32_t T1 = 0, above = 0, nbin = 0;
     int sh = 0;
     if (ok) {
-      // a bit window that spreads [lo, hi] over <= 1025 of the kUnionBins
-      // bins: (hi - lo) >> sh < 1024, so (hi >> sh) - (lo >> sh) <= 1024
+      // a bit window over [lo, hi], anchored at lo: bin (w - lo) >> sh,
+      // (hi - lo) >> sh < kUnionBins (the finer the bins, the fewer keys
+      // share the threshold bin)
       {
         const uint32_t d = hi - lo;
-        sh = d < 1024u ? 0 : 32 - __builtin_clz(d) - 10;
+        sh = d < (uint32_t)kUnionBins ? 0 : 32 - __builtin_clz(d) - 11;
       }
-      const uint32_t base = lo >> sh;
+      static_assert(kUnionBins == 2048, "the window shift keeps 11 bits");
       uint32_t* hist = cs.scan.hist;
       // branch-free: keys below lo land in spill bins past the histogram
       // (a spill word per lane: the lanes' atomics never collide)
       const uint32_t spill = kUnionWords + (uint32_t)(t & (kWave - 1));
-      for_mine([&](uint32_t w, uint32_t) { atomicAdd(&hist[w >= lo ? union_slot((w >> sh) - base) : spill], 1u); });
+      for_mine([&](uint32_t w, uint32_t) { atomicAdd(&hist[w >= lo ? union_slot((w - lo) >> sh) : spill], 1u); });
       __syncthreads();
       dbg_stamp(dbk, 12);
       const BinThreshold th = wave_threshold_sum<kUnionGroup, kUnionStride>(hist, (uint32_t)K);
       ok = th.total >= (uint32_t)K;  // the union holds at least K keys >= lo
-      T1 = th.bin + base;            // == t* >> sh
+      T1 = th.bin;                   // == (t* - lo) >> sh
       above = th.above;
       nbin = th.cnt;
     }
@@ -978,10 +983,10 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
     // pass 2: finite keys above T1's bin are selected: count them (and
     // those of the lists before this one; a list is a whole number of
     // uint4s); T1's bin -> candidates.  Edges: bin > T1 <=> w > top, and
-    // bin == T1 with w >= lo <=> bot <= w <= top.
-    const uint64_t top64 = (((uint64_t)T1 + 1u) << sh) - 1u;
+    // bin == T1 <=> bot <= w <= top.
+    const uint64_t top64 = (uint64_t)lo + (((uint64_t)T1 + 1u) << sh) - 1u;
     const uint32_t top = top64 > 0xffffffffull ? 0xffffffffu : (uint32_t)top64;
-    const uint32_t bot = max(lo, T1 << sh);
+    const uint32_t bot = lo + (T1 << sh);
     uint32_t ax = 0, az = 0, cmask = 0;
 #pragma unroll
     for (int j = 0; j < kU; ++j) {
@@ -1028,7 +1033,7 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
       sel_above += cs.pred[2 * w + 1];
     }
     const uint32_t nc = nbin;                   // == the candidates collected
-    dbg_value(dbk, 5, ((unsigned long long)nc << 32) | (uint32_t)sh);
+    // (value slot 27 holds the bound path)
     const uint32_t need = (uint32_t)K - above;  // 1 <= need <= nc
     if (nc <= (uint32_t)kWave) {
       // each wave: exact t* by rank counting (the candidate c with
@@ -1085,14 +1090,14 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
           __syncthreads();
           const int hs = s2 + sub;
           for_mine([&](uint32_t w, uint32_t) {
-            if (w >= lo && (w >> hs) == prefix) atomicAdd(&hist[(w >> s2) & ((1u << sub) - 1u)], 1u);
+            if (w >= lo && ((w - lo) >> hs) == prefix) atomicAdd(&hist[((w - lo) >> s2) & ((1u << sub) - 1u)], 1u);
           });
           __syncthreads();
           find_threshold_fixed<kNB2, kMainThreads>(hist, nd, cs.wave_tmp, cs.res);
           prefix = (prefix << sub) | cs.res[0];
           nd -= cs.res[1];
         }
-        tstar = prefix;
+        tstar = lo + prefix;
         need3 = nd;
       }
       // the bin-T1 keys' share (keys above the bin were counted in pass 2)
@@ -1108,7 +1113,7 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
         for (uint32_t j = t; j < nc; j += kMainThreads) count(cs.ck[j], cs.ce[j]);
       } else {
         for_mine([&](uint32_t w, uint32_t e) {
-          if (w >= lo && (w >> sh) == T1) count(w, e);
+          if (w >= lo && ((w - lo) >> sh) == T1) count(w, e);
         });
       }
       const uint4 r = block_reduce4<0, 0, 0, 0>(acc, cs.wave_tmp);
@@ -1212,6 +1217,14 @@ __device__ __forceinline__ v4f qk_fp8(const v8i& qa, const v8i& kb) {
   return acc;
 }
 
+// Workgroup i's share [part(n, i, nb), part(n, i + 1, nb)) of n items, in
+// 32-bit unsigned arithmetic (a 64-bit division is ~100 instructions, and
+// every instruction on this serial path costs ~2 ns): n * nb < 2^32, which
+// the launcher checks.
+__device__ __forceinline__ int part(int n, int i, int nb) {
+  return (int)(((uint32_t)n * (uint32_t)i) / (uint32_t)nb);
+}
+
 // FROM_SCORES: the row's scores are already in the slab (a plain scan
 // launch wrote them); the workgroup loads its positions' scores instead of
 // scoring the keys, then selects as usual.
@@ -1232,7 +1245,7 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   // query, speculating that the row is full (len == cap, the usual decode
   // case) so the prefetch need not wait for seq_lens; a shorter row reloads.
   const int ncap = (cap + kChunkKeys - 1) / kChunkKeys;
-  const int sc0 = (int)((long)ncap * bid / nb), sc1 = (int)((long)ncap * (bid + 1) / nb);
+  const int sc0 = part(ncap, bid, nb), sc1 = part(ncap, bid + 1, nb);
   const int spg0 = sc0 >> 2;
   const int snpg = (sc1 > sc0) ? ((sc1 - 1) >> 2) - spg0 + 1 : 0;
   constexpr int kQ = FROM_SCORES ? 0 : kHeads * DSA_INDEX_DIM / 16;  // uint4 of the query block
@@ -1241,16 +1254,19 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   if (t < kQ) qv = qsrc[t];
   const float wv0 = (!FROM_SCORES && t < kHeads) ? S.w[(long)row * kHeads + t] : 0.f;
   const int spv = (has_pt && snpg <= kMainThreads && t < snpg) ? pt_row[spg0 + t] : 0;
+  dbg_stamp(dbk, 28);
   const int len = max(0, min(S.seq_lens[row], cap));
   const int nchunks = (len + kChunkKeys - 1) / kChunkKeys;
-  const int c0 = (int)((long)nchunks * bid / nb);
-  const int c1 = (int)((long)nchunks * (bid + 1) / nb);
+  const int c0 = part(nchunks, bid, nb);
+  const int c1 = part(nchunks, bid + 1, nb);
   const int pg0 = c0 >> 2;
   const int npg = (c1 > c0) ? ((c1 - 1) >> 2) - pg0 + 1 : 0;
   const bool pts_lds = has_pt && npg <= kScanMaxPages;
   {
     const bool spec_ok = nchunks == ncap && snpg <= kMainThreads;  // then pg0, npg == spg0, snpg
+    dbg_stamp(dbk, 29);
     if (t < kQ) reinterpret_cast<uint4*>(sh.qs)[t] = qv;
+    dbg_stamp(dbk, 30);
     for (int i = t + kMainThreads; i < kQ; i += kMainThreads) reinterpret_cast<uint4*>(sh.qs)[i] = qsrc[i];
     if (!FROM_SCORES && t < kHeads) sh.ws[t] = wv0;
     if (pts_lds) {
@@ -1261,7 +1277,7 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
       }
     }
     if (with_hist)
-      for (int i = t; i < kHistWords; i += kMainThreads) sh.hist[i] = 0u;
+      for (int i = t; i < kHistWords / 4; i += kMainThreads) reinterpret_cast<uint4*>(sh.hist)[i] = make_uint4(0, 0, 0, 0);
   }
   // the row barriers' flag values (flipped once per use), read now and
   // stored for the select after the scan (the loads' latency hides under it)
@@ -1281,6 +1297,7 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
       }
     }
   }
+  dbg_stamp(dbk, 31);
   __syncthreads();
 
   dbg_stamp(dbk, 1);
@@ -1328,8 +1345,8 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   }
 
   const int n = c1 - c0;
-  const int w0 = c0 + (int)((long)n * wv / kMainWaves);
-  const int w1 = c0 + (int)((long)n * (wv + 1) / kMainWaves);
+  const int w0 = c0 + (int)((uint32_t)(n * wv) / kMainWaves);
+  const int w1 = c0 + (int)((uint32_t)(n * (wv + 1)) / kMainWaves);
   constexpr int kScanBatch = scan_batch<SELECT>();
   // One batch of chunks per step, every load issued before any is used.
   // Branch-free: each chunk reads through a buffer resource over its page
@@ -1404,7 +1421,7 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
     run_chunks(std::false_type{});
   }  // !FROM_SCORES
   dbg_stamp(dbk, 2);
-  dbg_stamp_wave(dbk, 5, kMainWaves - 1);
+  dbg_stamp_lane0(16 + wave_id());
   if (!with_hist) return;
   if constexpr (SELECT) {
     if (S.coop) {
@@ -1722,6 +1739,10 @@ hipError_t launch_decode_main(const AttnArgs* A, int B_att, const ScanArgs* S, i
     sc.rows = B_scan;
     sc.balance = B_scan > 1 && B_scan <= kWave;
     sc.max_nb = sc.coop ? (int)std::min<long>(kCoopMaxBlocks, device_cus() - 8) : n_scan;
+    // the workgroups split a row's chunks in 32-bit arithmetic (part())
+    const long cap_chunks =
+        (std::min((long)sc.slab_stride, (long)sc.pt_stride * DSA_PAGE_TOKENS) + kChunkKeys - 1) / kChunkKeys;
+    if ((cap_chunks + 1) * (long)std::max(sc.max_nb, sc.blocks_per_row) >= (1L << 32)) return hipErrorInvalidValue;
     // one round of workgroups: when the launch's LDS pins one workgroup per
     // CU, the CUs the attention leaves (spare workgroups exit at once)
     const bool big_lds = n_att > 0 || select;

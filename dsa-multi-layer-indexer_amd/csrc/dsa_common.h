@@ -144,6 +144,55 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Phase timestamps for profiling, compiled in only with -DDSA_PHASE_STAMPS
+// (each stamp reads the enable flag from memory and waits for it, which
+// would put a memory round trip on the critical path of every phase):
+// thread 0 of workgroup `blk` records the 100 MHz constant clock at phase
+// `ph`; the internal dsa_internal_debug entry point clears the table.
+// Counterpart of the reference's hp_dbg stamps (K:1076-1091).
+constexpr int kDbgBlocks = 512;
+constexpr int kDbgPhases = 32;
+extern __device__ int g_dbg_on;
+extern __device__ unsigned long long g_dbg[kDbgBlocks * kDbgPhases];
+#ifdef DSA_PHASE_STAMPS
+// Profiling builds record into LDS (no memory traffic, so a stamp does not
+// delay the launch's own waits for its loads and stores) and copy the
+// workgroup's stamps to g_dbg once, at its end (dbg_flush).
+constexpr bool kPhaseStamps = true;
+__shared__ unsigned long long s_dbg_marks[kDbgPhases];
+__device__ __forceinline__ void dbg_begin() {
+  if (threadIdx.x < kDbgPhases) s_dbg_marks[threadIdx.x] = 0ull;
+}
+__device__ __forceinline__ void dbg_stamp(int, int ph) {
+  if (threadIdx.x == 0) s_dbg_marks[ph] = __builtin_amdgcn_s_memrealtime();
+}
+// Same, recorded by lane 0 of wave `w` instead of thread 0.
+__device__ __forceinline__ void dbg_stamp_wave(int, int ph, int w) {
+  if (threadIdx.x == (unsigned)(w * kWave)) s_dbg_marks[ph] = __builtin_amdgcn_s_memrealtime();
+}
+// Same, recorded by lane 0 of every wave that calls it.
+__device__ __forceinline__ void dbg_stamp_lane0(int ph) {
+  if ((threadIdx.x & (kWave - 1)) == 0) s_dbg_marks[ph] = __builtin_amdgcn_s_memrealtime();
+}
+// a value instead of a time (the probe reads it from the same table)
+__device__ __forceinline__ void dbg_value(int, int ph, unsigned long long v) {
+  if (threadIdx.x == 0) s_dbg_marks[ph] = v;
+}
+// every thread of the workgroup calls it once, at the end
+__device__ __forceinline__ void dbg_flush(int blk) {
+  __syncthreads();
+  if (threadIdx.x < kDbgPhases && blk < kDbgBlocks) g_dbg[blk * kDbgPhases + threadIdx.x] = s_dbg_marks[threadIdx.x];
+}
+#else
+constexpr bool kPhaseStamps = false;
+__device__ __forceinline__ void dbg_begin() {}
+__device__ __forceinline__ void dbg_flush(int) {}
+__device__ __forceinline__ void dbg_value(int, int, unsigned long long) {}
+__device__ __forceinline__ void dbg_stamp(int, int) {}
+__device__ __forceinline__ void dbg_stamp_wave(int, int, int) {}
+__device__ __forceinline__ void dbg_stamp_lane0(int) {}
+#endif
+
 // ---- device-coherent publication between workgroups of one launch ----
 // Data a workgroup hands to the "last arriving" workgroup of its group is
 // written with device-scope stores (global_store ... sc1: coherent across
@@ -217,7 +266,9 @@ __device__ __forceinline__ void group_barrier_rep(uint32_t* sync, uint32_t* tops
                                                   uint32_t sense) {
   const uint32_t set = sense & 1u;
   wait_mem();
+  dbg_stamp(0, 23);
   __syncthreads();
+  dbg_stamp(0, 24);
   if (threadIdx.x == 0) {
     const int g = bid % kRepGroups;
     const uint32_t ng = (uint32_t)((nb - 1 - g) / kRepGroups + 1);
@@ -326,48 +377,5 @@ __device__ __forceinline__ uint4 block_reduce4(uint4 v, uint32_t* wave_tmp) {
   return r;
 }
 
-// Phase timestamps for profiling, compiled in only with -DDSA_PHASE_STAMPS
-// (each stamp reads the enable flag from memory and waits for it, which
-// would put a memory round trip on the critical path of every phase):
-// thread 0 of workgroup `blk` records the 100 MHz constant clock at phase
-// `ph`; the internal dsa_internal_debug entry point clears the table.
-// Counterpart of the reference's hp_dbg stamps (K:1076-1091).
-constexpr int kDbgBlocks = 512;
-constexpr int kDbgPhases = 16;
-extern __device__ int g_dbg_on;
-extern __device__ unsigned long long g_dbg[kDbgBlocks * kDbgPhases];
-#ifdef DSA_PHASE_STAMPS
-// Profiling builds record into LDS (no memory traffic, so a stamp does not
-// delay the launch's own waits for its loads and stores) and copy the
-// workgroup's stamps to g_dbg once, at its end (dbg_flush).
-constexpr bool kPhaseStamps = true;
-__shared__ unsigned long long s_dbg_marks[kDbgPhases];
-__device__ __forceinline__ void dbg_begin() {
-  if (threadIdx.x < kDbgPhases) s_dbg_marks[threadIdx.x] = 0ull;
-}
-__device__ __forceinline__ void dbg_stamp(int, int ph) {
-  if (threadIdx.x == 0) s_dbg_marks[ph] = __builtin_amdgcn_s_memrealtime();
-}
-// Same, recorded by lane 0 of wave `w` instead of thread 0.
-__device__ __forceinline__ void dbg_stamp_wave(int, int ph, int w) {
-  if (threadIdx.x == (unsigned)(w * kWave)) s_dbg_marks[ph] = __builtin_amdgcn_s_memrealtime();
-}
-// a value instead of a time (the probe reads it from the same table)
-__device__ __forceinline__ void dbg_value(int, int ph, unsigned long long v) {
-  if (threadIdx.x == 0) s_dbg_marks[ph] = v;
-}
-// every thread of the workgroup calls it once, at the end
-__device__ __forceinline__ void dbg_flush(int blk) {
-  __syncthreads();
-  if (threadIdx.x < kDbgPhases && blk < kDbgBlocks) g_dbg[blk * kDbgPhases + threadIdx.x] = s_dbg_marks[threadIdx.x];
-}
-#else
-constexpr bool kPhaseStamps = false;
-__device__ __forceinline__ void dbg_begin() {}
-__device__ __forceinline__ void dbg_flush(int) {}
-__device__ __forceinline__ void dbg_value(int, int, unsigned long long) {}
-__device__ __forceinline__ void dbg_stamp(int, int) {}
-__device__ __forceinline__ void dbg_stamp_wave(int, int, int) {}
-#endif
 
 }  // namespace dsa
