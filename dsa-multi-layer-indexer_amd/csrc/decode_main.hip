@@ -469,7 +469,6 @@ struct CoopShared {
   alignas(16) uint32_t ck[kCoopCand];  // threshold-bin candidates: key, union entry index
   uint32_t ce[kCoopCand];
   uint32_t wstat[2 * kMainWaves];  // per wave, from the scan: finite keys, largest key
-  uint32_t hred[2 * kMainWaves];   // per wave: list-header reductions
   uint32_t pred[2 * kMainWaves];   // per wave: union counts of pass 2
 };
 
@@ -877,51 +876,51 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
     }
   }
   dbg_stamp(dbk, 8);
-  group_barrier_rep(sync, sync + 3 * kSyncWords, bid, nb, cs.sense[0]);
+  group_arrive_rep(sync, sync + 3 * kSyncWords, bid, nb, cs.sense[0]);
+  // while the other workgroups arrive: clear what the union steps count
+  // (the scan's histogram is no longer needed)
+  static_assert(kUnionWords % 4 == 0 && kUnionWords <= 8 * kMainThreads, "union histogram clear");
+  for (int i = t; i < kUnionWords / 4; i += kMainThreads)
+    reinterpret_cast<uint4*>(cs.scan.hist)[i] = make_uint4(0, 0, 0, 0);
+  if (t < kWave) cs.ck[t] = 0u;  // candidates past the count read as 0
+  if (t == 0) cs.misc[1] = 0u;
+  group_wait_rep(sync, sync + 3 * kSyncWords, bid, nb, cs.sense[0]);
   dbg_stamp(dbk, 9);
 
   // ---- every workgroup: all lists into registers (one batch of
-  // device-scope loads; thread t holds uint4s t, t + 512, ... of the area)
-  // and the headers' reductions ----
+  // device-scope loads; thread t holds uint4s t, t + 512, ... of the area);
+  // every wave loads all headers (lane l: l, l + 64, ...) and reduces them
+  // itself, so no block step is needed ----
   const int nent = all ? 0 : nb * P;
   constexpr int kU = NU;
   static_assert(NU * 4 * kMainThreads <= kPubWords, "union registers");
+  static_assert(kCoopMaxBlocks <= 4 * kWave, "headers: 4 per lane");
   uint4 u[kU];
+  uint32_t h0 = 0, h1 = 0;
   {
-    uint32_t hdr_b = 0, hdr_f = 0, hdr_m = 0;
     const __amdgpu_buffer_rsrc_t r = dev_rsrc(gpub, 4u * (uint32_t)nent);
-    if (t < nb) {
-      const uint4 h = load_dev16(dev_rsrc(ghdr, 16u * (uint32_t)nb), 16u * t);
-      hdr_b = h.y;
-      hdr_f = h.z;
-      hdr_m = h.w;
-    }
+    const __amdgpu_buffer_rsrc_t hr = dev_rsrc(ghdr, 16u * (uint32_t)nb);
+    uint4 h[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) h[k] = load_dev16(hr, 16u * (uint32_t)(lane + k * kWave));  // 0 past nb
 #pragma unroll
     for (int j = 0; j < kU; ++j) {
       const int i = t + j * kMainThreads;
       u[j] = load_dev16(r, 16u * i);  // 0 past the end of the resource
     }
-    for (int i = t; i < kUnionWords; i += kMainThreads) cs.scan.hist[i] = 0u;
-    if (t < kWave) cs.ck[t] = 0u;  // candidates past the count read as 0
     // all: (finite keys of the lists before this one, of all lists);
     // else: (largest bound, largest key)
-    const uint32_t r0 = all ? wave_reduce<0>(t < bid ? hdr_f : 0u) : wave_reduce<2>(hdr_b);
-    const uint32_t r1 = all ? wave_reduce<0>(hdr_f) : wave_reduce<2>(hdr_m);
-    if (lane == 0) {
-      cs.hred[2 * wv] = r0;
-      cs.hred[2 * wv + 1] = r1;
-    }
-  }
-  if (t == 0) cs.misc[1] = 0u;
-  __syncthreads();
-  dbg_stamp(dbk, 10);
-  uint32_t h0 = 0, h1 = 0;
+    uint32_t a = 0, b = 0;
 #pragma unroll
-  for (int w = 0; w < kMainWaves; ++w) {
-    const uint32_t a = cs.hred[2 * w], b = cs.hred[2 * w + 1];
-    h0 = all ? h0 + a : max(h0, a);
-    h1 = all ? h1 + b : max(h1, b);
+    for (int k = 0; k < 4; ++k) {
+      const int j = lane + k * kWave;
+      a = all ? a + (j < bid ? h[k].z : 0u) : max(a, h[k].y);
+      b = all ? b + h[k].z : max(b, h[k].w);
+    }
+    h0 = all ? wave_reduce<0>(a) : wave_reduce<2>(a);
+    h1 = all ? wave_reduce<0>(b) : wave_reduce<2>(b);
   }
+  dbg_stamp(dbk, 10);
   // f(word, union index) over this thread's words (zeros past the end: below
   // every bound)
   const auto for_mine = [&](auto&& f) {
@@ -1360,44 +1359,75 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
     constexpr bool kPtLds = decltype(pt_lds)::value;
     for (int cb = w0; cb < w1; cb += kScanBatch) {
       uint4 kv[kScanBatch][2];
-      float ksc[kScanBatch];
-      bool ok[kScanBatch];
+      int pgs[kScanBatch];  // the chunk's page, -1 when it has none (uniform)
 #pragma unroll
       for (int i = 0; i < kScanBatch; ++i) {
         const int c = min(cb + i, w1 - 1);
         const int pg = __builtin_amdgcn_readfirstlane(kPtLds ? sh.pts[(c >> 2) - pg0] : pt_row[c >> 2]);
-        ok[i] = cb + i < w1 && pg >= 0 && (long)pg < S.num_pages;
+        const bool ok = cb + i < w1 && pg >= 0 && (long)pg < S.num_pages;
+        pgs[i] = ok ? pg : -1;
         const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t*>(S.pages) + (ok[i] ? (long)pg * DSA_INDEX_PAGE_BYTES : 0L), (short)0,
-            ok[i] ? DSA_INDEX_PAGE_BYTES : 0, 0x00020000);
+            const_cast<uint8_t*>(S.pages) + (ok ? (long)pg * DSA_INDEX_PAGE_BYTES : 0L), (short)0,
+            ok ? DSA_INDEX_PAGE_BYTES : 0, 0x00020000);
         const int off = (c & 3) * (kChunkKeys * DSA_INDEX_DIM) + kr * DSA_INDEX_DIM + kc * 32;
         kv[i][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
         kv[i][1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off + 16, 0, 0));
-        ksc[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-            r, DSA_PAGE_TOKENS * DSA_INDEX_DIM + ((c & 3) * kChunkKeys + kr) * 4, 0, 0));
       }
+      // the key scales in the layout of the reduced scores: lane (j, kr) of
+      // group q loads key kr's scale of chunk 4q + j (one load per group;
+      // 0 for a chunk without a page)
+      float ksl[kScanBatch / 4];
 #pragma unroll
-      for (int i = 0; i < kScanBatch; ++i) {
-        const int c = cb + i;
-        if (c >= w1) break;  // uniform
-        const v8i kb = v8i{(int)kv[i][0].x, (int)kv[i][0].y, (int)kv[i][0].z, (int)kv[i][0].w,
-                           (int)kv[i][1].x, (int)kv[i][1].y, (int)kv[i][1].z, (int)kv[i][1].w};
-        float acc = 0.f;  // an invalid chunk's zero keys give 0
+      for (int q = 0; q < kScanBatch / 4; ++q) {
+        const int pl = kc == 0 ? pgs[4 * q] : (kc == 1 ? pgs[4 * q + 1] : (kc == 2 ? pgs[4 * q + 2] : pgs[4 * q + 3]));
+        const int cl = cb + 4 * q + kc;
+        const float* sp = reinterpret_cast<const float*>(S.pages + (long)max(pl, 0) * DSA_INDEX_PAGE_BYTES +
+                                                         DSA_PAGE_TOKENS * DSA_INDEX_DIM) +
+                          (cl & 3) * kChunkKeys + kr;
+        ksl[q] = pl >= 0 ? *sp : 0.f;
+      }
+      // Groups of 4 chunks: each lane sums ReLU*w over its 16 heads of
+      // every chunk, then two rounds of lane swaps transpose-reduce the
+      // four 16-lane groups so that lane (j, kr) ends with key kr of chunk
+      // 4q + j -- the same additions in the same order as reducing each
+      // chunk into lanes 0-15 (+ lane i+32, then + lane i+16), with 3 swaps
+      // and 3 adds per 4 chunks, and the per-key tail below runs once per
+      // group on all 64 lanes.
+      static_assert(kScanBatch % 4 == 0, "chunks are reduced in groups of 4");
 #pragma unroll
-        for (int hg = 0; hg < NHG; ++hg) {
-          const v4f d = qk_fp8<VARIANT>(qa[hg], kb);
+      for (int q = 0; q < kScanBatch / 4; ++q) {
+        if (cb + 4 * q >= w1) break;  // uniform
+        float a[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc += wr[hg][r] * fmaxf(d[r], 0.f);
+        for (int j = 0; j < 4; ++j) {
+          const int i = 4 * q + j;
+          const v8i kb = v8i{(int)kv[i][0].x, (int)kv[i][0].y, (int)kv[i][0].z, (int)kv[i][0].w,
+                             (int)kv[i][1].x, (int)kv[i][1].y, (int)kv[i][1].z, (int)kv[i][1].w};
+          a[j] = 0.f;  // an invalid chunk's zero keys give 0
+          if (cb + i >= w1) continue;  // uniform: past the wave's chunks
+#pragma unroll
+          for (int hg = 0; hg < NHG; ++hg) {
+            const v4f d = qk_fp8<VARIANT>(qa[hg], kb);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) a[j] += wr[hg][r] * fmaxf(d[r], 0.f);
+          }
         }
-        // sum the four 16-lane groups into lanes 0-15 with lane swaps (VALU,
-        // no LDS round trip): + lane i+32, then + lane i+16
-        acc += __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(acc), __float_as_uint(acc),
-                                                                false, false)[1]);
-        acc += __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(acc), __float_as_uint(acc),
-                                                                false, false)[1]);
+        // permlane32_swap(x, y) -> {[x.lo, y.lo], [x.hi, y.hi]} (32-lane
+        // halves); permlane16_swap(x, y) -> {[x.r0, y.r0, x.r2, y.r2],
+        // [x.r1, y.r1, x.r3, y.r3]} (16-lane rows)
+        const auto add32 = [](float x, float y) {
+          const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+          return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        };
+        const float x = add32(a[0], a[2]);  // lanes 0-31: chunk 0; 32-63: chunk 2
+        const float y = add32(a[1], a[3]);  // chunks 1, 3
+        const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+        const float acc = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+        const int c = cb + 4 * q + kc;  // this lane's chunk
+        const bool okj = (kc == 0 ? pgs[4 * q] : (kc == 1 ? pgs[4 * q + 1] : (kc == 2 ? pgs[4 * q + 2] : pgs[4 * q + 3]))) >= 0;
         const int g = c * kChunkKeys + kr;
-        if (lane < 16 && g < S.slab_stride) {
-          const float v = (ok[i] && g < len) ? acc * ksc[i] : -INFINITY;
+        if (c < w1 && g < S.slab_stride) {
+          const float v = (okj && g < len) ? acc * ksl[q] : -INFINITY;
           // device-scope stores when the row's last workgroup reads them back
           if (S.next_idx) store_dev(&srow[g], v);
           else srow[g] = v;

@@ -249,7 +249,8 @@ __device__ __forceinline__ uint32_t group_sense(const uint32_t* sync, int bid) {
   return __hip_atomic_load(&sync[(kGroupSyncGroups + 1 + (bid & (kGroupSyncFlags - 1))) * kGroupSyncLine],
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// A group barrier with one atomic round trip on the last arrival's path.
+// A group barrier with one atomic round trip on the last arrival's path,
+// in two halves (group_arrive_rep, group_wait_rep).
 // Members arrive on kRepGroups group counters; a group's last arrival adds
 // itself, without waiting for the result, to kRepTops replicated top
 // counters, and every member polls the replica of its XCD until all groups
@@ -262,8 +263,11 @@ __device__ __forceinline__ uint32_t group_sense(const uint32_t* sync, int bid) {
 constexpr int kRepGroups = 8, kRepTops = 8;
 static_assert(2 * kRepGroups <= kGroupSyncGroups && 2 * kRepTops <= kGroupSyncGroups + 1,
               "two counter sets fit a barrier area");
-__device__ __forceinline__ void group_barrier_rep(uint32_t* sync, uint32_t* tops, int bid, int nb,
-                                                  uint32_t sense) {
+// Arrival half: publishes (waits for this workgroup's stores) and arrives.
+// The caller may do work that needs no other workgroup's data, then calls
+// group_wait_rep with the same arguments.
+__device__ __forceinline__ void group_arrive_rep(uint32_t* sync, uint32_t* tops, int bid, int nb,
+                                                 uint32_t sense) {
   const uint32_t set = sense & 1u;
   wait_mem();
   dbg_stamp(0, 23);
@@ -276,6 +280,12 @@ __device__ __forceinline__ void group_barrier_rep(uint32_t* sync, uint32_t* tops
       for (int r = 0; r < kRepTops; ++r)
         __hip_atomic_fetch_add(&tops[(set * kRepTops + r) * kGroupSyncLine], 1u, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+// Wait half: returns (to every thread) once all nb members have arrived.
+__device__ __forceinline__ void group_wait_rep(uint32_t* sync, uint32_t* tops, int bid, int nb, uint32_t sense) {
+  const uint32_t set = sense & 1u;
+  if (threadIdx.x == 0) {
     const uint32_t ngroups = (uint32_t)min(nb, kRepGroups);
     const uint32_t* top = &tops[(set * kRepTops + bid % kRepTops) * kGroupSyncLine];
     for (int i = 0; __hip_atomic_load(top, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < ngroups; ++i) {
