@@ -884,6 +884,20 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
     reinterpret_cast<uint4*>(cs.scan.hist)[i] = make_uint4(0, 0, 0, 0);
   if (t < kWave) cs.ck[t] = 0u;  // candidates past the count read as 0
   if (t == 0) cs.misc[1] = 0u;
+  // a list of at most one wave's entries is emitted by wave 0 (below): its
+  // lane l takes entry l, whose key and output slot are read now
+  const auto slot_of = [&](int p) {  // a position, or its KV slot when there is a page table
+    if (TOPK && !pt_row) return p;
+    return (pts_lds ? pts[(p >> 6) - pg0] : pt_row[p >> 6]) * DSA_PAGE_TOKENS + (p & (DSA_PAGE_TOKENS - 1));
+  };
+  const bool wave_emit = !all && cnt <= (uint32_t)kWave;
+  uint32_t em_key = 0;
+  int em_slot = 0;
+  if (wave_emit && wv == 0 && lane < (int)cnt) {
+    const int i = (int)lpos[lane];
+    em_key = cs.keys[i];
+    em_slot = slot_of(p_lo + i);
+  }
   group_wait_rep(sync, sync + 3 * kSyncWords, bid, nb, cs.sense[0]);
   dbg_stamp(dbk, 9);
 
@@ -1018,18 +1032,18 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
       }
     }
     dbg_stamp(dbk, 6);
-    ax = wave_reduce<0>(ax);
-    az = wave_reduce<0>(az);
-    if (lane == 0) {
-      cs.pred[2 * wv] = ax;
-      cs.pred[2 * wv + 1] = az;
-    }
+    // both counts in one reduction: each is at most the union's size
+    // (<= kPubWords < 2^16)
+    static_assert(kPubWords < 65536, "packed union counts");
+    const uint32_t axz = wave_reduce<0>(ax | az << 16);
+    if (lane == 0) cs.pred[wv] = axz;
     __syncthreads();
     dbg_stamp(dbk, 7);
 #pragma unroll
     for (int w = 0; w < kMainWaves; ++w) {
-      sel_before += cs.pred[2 * w];
-      sel_above += cs.pred[2 * w + 1];
+      const uint32_t v = cs.pred[w];
+      sel_before += v & 0xffffu;
+      sel_above += v >> 16;
     }
     const uint32_t nc = nbin;                   // == the candidates collected
     // (value slot 27 holds the bound path)
@@ -1132,22 +1146,17 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
   // entries in position order: thread t takes contiguous entries.  A row of
   // <= K tokens publishes nothing and takes every finite key instead. ----
   const int n_e = all ? nown : (int)cnt;
-  const auto slot_of = [&](int p) {  // a position, or its KV slot when there is a page table
-    if (TOPK && !pt_row) return p;
-    return (pts_lds ? pts[(p >> 6) - pg0] : pt_row[p >> 6]) * DSA_PAGE_TOKENS + (p & (DSA_PAGE_TOKENS - 1));
-  };
-  if (!all && n_e <= kWave) {
+  if (wave_emit) {
     // a list of at most one wave's entries: wave 0 emits it, ranks by ballot
     if (wv == 0) {
       const bool in = lane < n_e;
-      const int i = in ? (int)lpos[lane] : 0;
-      const uint32_t k = in ? cs.keys[i] : 0u;
+      const uint32_t k = em_key;
       const uint64_t below = (1ull << lane) - 1ull;
       const bool tie = in && tfin && k == tstar;
       const uint32_t tr = ties_before + (uint32_t)__popcll(__ballot(tie) & below);
       const bool sel = in && key_is_finite(k) && (k > tstar || (tie && tr < need3));
       const uint32_t pos = base + (uint32_t)__popcll(__ballot(sel) & below);
-      if (sel) o[min(pos, (uint32_t)K - 1u)] = slot_of(p_lo + i);  // < K by construction
+      if (sel) o[min(pos, (uint32_t)K - 1u)] = em_slot;  // < K by construction
     }
     if (bid == nb - 1)
       for (int j = (int)nsel + t; j < K; j += kMainThreads) o[j] = TOPK ? S.pad : -1;
