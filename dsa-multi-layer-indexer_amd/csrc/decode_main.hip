@@ -785,8 +785,10 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
   const int K = S.topk;
   const bool all = len <= K;
   const int nown = max(0, p_hi - p_lo);
-  const int P = pub_stride(nb, K);
-  const uint32_t M = (uint32_t)min(pub_target(nb, K), P);
+  // list stride and target: from the launcher when every row has the same
+  // workgroup count (two divisions fewer on this path), else per row
+  const int P = S.pub_stride ? S.pub_stride : pub_stride(nb, K);
+  const uint32_t M = (uint32_t)min(S.pub_stride ? S.pub_target : pub_target(nb, K), P);
   uint32_t* ghdr = rs + row_pub_off(S.slab_stride);  // [nb][kPubHdr]
   uint32_t* gpub = ghdr + kPubHdrWords;              // [nb][P] keys, zero-padded
   uint32_t* sync = rs + row_sync_off(S.slab_stride);
@@ -1778,6 +1780,9 @@ hipError_t launch_decode_main(const AttnArgs* A, int B_att, const ScanArgs* S, i
     sc.rows = B_scan;
     sc.balance = B_scan > 1 && B_scan <= kWave;
     sc.max_nb = sc.coop ? (int)std::min<long>(kCoopMaxBlocks, device_cus() - 8) : n_scan;
+    // one workgroup count for every row: the select's list sizing is fixed
+    sc.pub_stride = sc.coop && !sc.balance ? pub_stride(sc.blocks_per_row, sc.topk) : 0;
+    sc.pub_target = sc.coop && !sc.balance ? pub_target(sc.blocks_per_row, sc.topk) : 0;
     // the workgroups split a row's chunks in 32-bit arithmetic (part())
     const long cap_chunks =
         (std::min((long)sc.slab_stride, (long)sc.pt_stride * DSA_PAGE_TOKENS) + kChunkKeys - 1) / kChunkKeys;

@@ -53,6 +53,8 @@ struct ScanArgs {
   int standalone;        // with from_scores: the top-k op alone (pad below;
                          // page_table may be null: positions are emitted)
   int pad;               // standalone: value of the unused output entries
+  int pub_stride;        // filled by the launcher: cooperative-select list
+  int pub_target;        // stride and target (0: computed per row)
 };
 
 // One grid with n attention blocks (A != nullptr, rows B_att) and scan blocks
