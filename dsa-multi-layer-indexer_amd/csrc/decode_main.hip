@@ -4,16 +4,16 @@
 // Roles by blockIdx.x (role-decoupled workgroups, as the reference's HIDE
 // kernel does, K:1047-1070):
 //   [0, n_att)         attention: (row, head group, split) of split-K sparse
-//                      MLA; the last workgroup of a (row, head group) to
-//                      finish merges the splits (log-sum-exp) into the
-//                      output -- an arrival counter, no waiting;
+//                      MLA; the splits of a (row, head group) pass a group
+//                      barrier, then each merges (log-sum-exp) a 1/nsplit
+//                      slice of the outputs;
 //   [n_att, +n_scan)   indexer scan: (row, slice) of the row's 16-key
-//                      chunks; adds its scores' 12-bit key histogram to the
-//                      row's top-k histogram, and the row's last scan
-//                      workgroup to finish (arrival counter) runs the
-//                      row's whole top-k select (topk.hip finalize_row,
-//                      one pass over the scores) while attention blocks
-//                      are still gathering.
+//                      chunks; the row's scan workgroups then select its
+//                      top-k together (coop_select: each publishes a short
+//                      list of its top keys, and after one barrier every
+//                      workgroup finds the exact threshold from the lists
+//                      and writes its own selected positions), while the
+//                      attention workgroups are still busy.
 // Under the MLI lag, layer L's attention (over layer L-1's selection) and
 // layer L's indexer scan are independent, so one grid runs both and the
 // scan's HBM stream hides under the attention's gather latency.  Measured on
@@ -454,14 +454,7 @@ constexpr int kCoopCand = 1024;      // threshold-bin candidates resolved by ran
 struct CoopShared {
   ScanShared scan;
   uint32_t keys[kCoopKeys];
-  union {
-    struct {
-      uint32_t cand_key[kCandCap];  // the histogram form's threshold-bin candidates
-      int cand_idx[kCandCap];
-    };
-    uint16_t lpos[kPubWords];  // the list form's published entries: own position index
-  };
-  uint32_t gts[kCoopMaxBlocks];
+  uint16_t lpos[kPubWords];  // the published entries: own position index
   uint32_t wave_tmp[4 * kMainWaves];
   uint32_t res[4];
   uint32_t misc[4];
@@ -481,209 +474,15 @@ static_assert(kCoopKeys <= 65536, "own positions are stored as 16-bit indices");
 // it is split by sub-bins); every workgroup loads every list after the
 // barrier, so capacity costs load time.
 // A list too short for its workgroup only costs the fallback to the
-// histogram form.
+// single-workgroup select.
 __host__ __device__ inline int pub_target(int nb, int K) { return 2 * (int)(((uint32_t)K + nb - 1) / (uint32_t)nb) + 8; }
 __host__ __device__ inline int pub_stride(int nb, int K) {
   const int want = pub_target(nb, K) + (int)((((uint32_t)K + nb - 1) / (uint32_t)nb + 1) / 2);
   return min((want + 3) & ~3, (int)((uint32_t)kPubWords / (uint32_t)nb) & ~3);
 }
 
-// Histogram form of the cooperative select (the general case; the
-// published-list form below hands a row here when its lists cannot decide).
-// All nb scan workgroups of the row (co-resident: the launcher guarantees
-// nb fits the device), each holding the keys of its contiguous positions
-// [p_lo, p_hi), add their 12-bit key histograms to the row's, then:
-//   barrier 1 (histogram complete) -> every workgroup derives the threshold
-//     bin T1, counts its finite keys above T1 and appends its bin-T1 keys to
-//     the row's candidate list;
-//   barrier 2 (counts and candidates complete) -> every workgroup refines
-//     the exact threshold key t* from the candidates (same result in each),
-//     computes its output offset from the counts of the workgroups before it
-//     and the candidates before p_lo, and writes its own selected positions
-//     (KV slots) in position order; ties at t* go to the lowest positions.
-// A candidate list that would overflow (more than kCandCap keys in bin T1,
-// e.g. many equal scores) hands the row to the single-workgroup select
-// instead.  The last workgroup to finish re-arms the row's scratch.
-template <bool TOPK>
-__device__ __forceinline__ void coop_select_hist(CoopShared& cs, unsigned char* smem, const ScanArgs& S,
-                                                 int bid, int nb, int len, int p_lo, int p_hi, uint32_t* rs,
-                                                 const float* srow, const int* pt_row, int* o) {
-  const int t = threadIdx.x;
-  const int K = S.topk;
-  const bool all = len <= K;
-  const int nown = max(0, p_hi - p_lo);
-  {  // this workgroup's histogram into the row's
-    for (int i = t; i < kNB1; i += kMainThreads) cs.scan.hist[i] = 0u;
-    __syncthreads();
-    for (int i = t; i < nown; i += kMainThreads) atomicAdd(&cs.scan.hist[cs.keys[i] >> 20], 1u);
-    __syncthreads();
-    for (int i = t; i < kNB1; i += kMainThreads) {
-      const uint32_t c = cs.scan.hist[i];
-      if (c) atomicAdd(&rs[kHistOff + i], c);
-    }
-  }
-  uint32_t* gcount = rs + kBmOff;                               // [nb]
-  uint32_t* gcand = rs + kBmOff + bitmap_words(S.slab_stride);  // keys [cap], positions [cap]
-  uint32_t* sync = rs + row_sync_off(S.slab_stride);             // barriers 0 (lists), 1, 2
-  const int dbk = blockIdx.x;
-
-  uint32_t T1 = 0, above = 0, in_bin = 0;
-  if (!all) {
-    group_barrier(sync + kSyncWords, bid, nb, cs.sense[1]);
-    dbg_stamp(dbk, 8);
-    copy_words_to_lds<kNB1 / 4 / kMainThreads, true>(cs.scan.hist, rs + kHistOff, kNB1);
-    __syncthreads();
-    find_threshold(cs.scan.hist, kNB1, (uint32_t)K, cs.wave_tmp, cs.res);
-    T1 = cs.res[0];
-    above = cs.res[1];
-    in_bin = cs.scan.hist[T1];
-    dbg_stamp(dbk, 9);
-  }
-  if (in_bin > (uint32_t)kCandCap) {
-    // single-workgroup fallback (it re-arms the histogram and count)
-    if (bid != nb - 1) return;
-    __syncthreads();
-    FinShared& fs = *reinterpret_cast<FinShared*>(smem);
-    finalize_row(fs, srow, len, pt_row, S.pt_stride, rs, o, S.slab_stride, K, 0, TOPK ? S.pad : -1,
-                 /*fused=*/true);
-    return;
-  }
-
-  // ---- filter own positions: count, collect bin-T1 candidates ----
-  if (t == 0) cs.misc[0] = 0u;
-  __syncthreads();
-  uint32_t gt = 0;
-  for (int i = t; i < nown; i += kMainThreads) {
-    const uint32_t k = cs.keys[i];
-    const uint32_t bin = k >> 20;
-    const bool fin = key_is_finite(k);
-    if (all) {
-      gt += fin;
-    } else {
-      gt += (bin > T1 && fin) ? 1u : 0u;
-      if (bin == T1) {
-        const uint32_t slot = atomicAdd(&cs.misc[0], 1u);
-        cs.cand_key[slot] = k;
-        cs.cand_idx[slot] = p_lo + i;
-      }
-    }
-  }
-  const uint4 red = block_reduce4<0, 0, 0, 0>(make_uint4(gt, 0, 0, 0), cs.wave_tmp);
-  if (t == 0) {
-    const uint32_t nmine = cs.misc[0];
-    cs.misc[1] = nmine ? atomicAdd(&rs[kCntOff], nmine) : 0u;
-    store_dev(&gcount[bid], red.x);
-  }
-  __syncthreads();
-  {
-    const uint32_t nmine = cs.misc[0], base = cs.misc[1];
-    for (uint32_t i = t; i < nmine; i += kMainThreads) {
-      store_dev(&gcand[base + i], cs.cand_key[i]);
-      store_dev(&gcand[kCandCap + base + i], (uint32_t)cs.cand_idx[i]);
-    }
-  }
-  group_barrier(sync + 2 * kSyncWords, bid, nb, cs.sense[2]);
-  dbg_stamp(dbk, 10);
-
-  // ---- every workgroup: candidates, counts, exact threshold ----
-  const int nc = (int)in_bin;
-  {  // candidates (keys, positions) and the per-workgroup counts: one batch of loads
-    constexpr int kP = kCandCap / 4 / kMainThreads;
-    const __amdgpu_buffer_rsrc_t cr = dev_rsrc(gcand, 8u * kCandCap);
-    const __amdgpu_buffer_rsrc_t gr = dev_rsrc(gcount, 4u * (uint32_t)nb);
-    const int nc4 = all ? 0 : (nc + 3) >> 2;
-    uint4 ka[kP], ia[kP];
-    uint32_t gv = 0;
-#pragma unroll
-    for (int j = 0; j < kP; ++j) {
-      const int i = t + j * kMainThreads;
-      if (i < nc4) {
-        ka[j] = load_dev16(cr, 16u * i);
-        ia[j] = load_dev16(cr, 4u * kCandCap + 16u * i);
-      }
-    }
-    if (t < nb) gv = load_dev4(gr, 4u * t);
-#pragma unroll
-    for (int j = 0; j < kP; ++j) {
-      const int i = t + j * kMainThreads;
-      if (i < nc4) {
-        reinterpret_cast<uint4*>(cs.cand_key)[i] = ka[j];
-        reinterpret_cast<uint4*>(cs.cand_idx)[i] = ia[j];
-      }
-    }
-    if (t < nb) cs.gts[t] = gv;
-  }
-  for (int i = t; i < kNB2; i += kMainThreads) cs.scan.hist[i] = 0u;
-  __syncthreads();
-  dbg_stamp(dbk, 13);
-  uint32_t tstar = 0, need3 = 0;
-  if (!all)
-    refine_candidates(cs.cand_key, nc, T1, (uint32_t)K - above, cs.scan.hist, cs.wave_tmp, cs.res,
-                      tstar, need3);
-  const bool tfin = !all && key_is_finite(tstar);
-  dbg_stamp(dbk, 14);
-  // x: counts of workgroups before this one, y: all counts,
-  // z: candidates above t* before p_lo, w: ties before p_lo; then above t* in all
-  uint4 acc = make_uint4(0, 0, 0, 0);
-  uint32_t c_gt_all = 0;
-  if (t < nb) {
-    const uint32_t c = cs.gts[t];
-    acc.x = (t < bid) ? c : 0u;
-    acc.y = c;
-  }
-  for (int j = t; j < nc; j += kMainThreads) {
-    const uint32_t k = cs.cand_key[j];
-    const bool g = k > tstar && key_is_finite(k);
-    const bool before = cs.cand_idx[j] < p_lo;
-    acc.z += (g && before) ? 1u : 0u;
-    acc.w += (k == tstar && before) ? 1u : 0u;
-    c_gt_all += g ? 1u : 0u;
-  }
-  const uint4 r1 = block_reduce4<0, 0, 0, 0>(acc, cs.wave_tmp);
-  const uint4 r2 = block_reduce4<0, 0, 0, 0>(make_uint4(c_gt_all, 0, 0, 0), cs.wave_tmp);
-  const uint32_t ties_before = r1.w;
-  const uint32_t base = r1.x + r1.z + (tfin ? min(ties_before, need3) : 0u);
-  const uint32_t nsel = r1.y + r2.x + (tfin ? need3 : 0u);
-  dbg_stamp(dbk, 11);
-
-  // ---- emit own selections in position order ----
-  uint32_t run_sel = 0, run_tie = ties_before;
-  for (int i0 = 0; i0 < nown; i0 += kMainThreads) {
-    const int i = i0 + t;
-    const bool in = i < nown;
-    const uint32_t k = in ? cs.keys[i] : 0u;
-    const bool tie = in && tfin && k == tstar;
-    uint32_t tie_tot = 0, sel_tot;
-    uint32_t tie_pre = 0;
-    if (__syncthreads_or(tie)) tie_pre = block_flag_scan(tie, cs.wave_tmp, &tie_tot);
-    bool sel;
-    if (all) {
-      sel = in && key_is_finite(k);
-    } else {
-      const uint32_t bin = k >> 20;
-      sel = in && key_is_finite(k) &&
-            (bin > T1 || (bin == T1 && (k > tstar || (tie && run_tie + tie_pre < need3))));
-    }
-    const uint32_t sel_pre = block_flag_scan(sel, cs.wave_tmp, &sel_tot);
-    if (sel) {  // the slot is < K by construction; clamped anyway
-      const int p = p_lo + i;
-      o[min(base + run_sel + sel_pre, (uint32_t)K - 1u)] =
-          (TOPK && !pt_row) ? p : pt_row[p >> 6] * DSA_PAGE_TOKENS + (p & (DSA_PAGE_TOKENS - 1));
-    }
-    run_sel += sel_tot;
-    run_tie += tie_tot;
-  }
-  if (bid == nb - 1)
-    for (int j = (int)nsel + t; j < K; j += kMainThreads) o[j] = TOPK ? S.pad : -1;
-
-  // ---- re-arm: everyone has read the histogram (barrier 2 passed) ----
-  for (int i = kNB1 * bid / nb + t; i < kNB1 * (bid + 1) / nb; i += kMainThreads) rs[kHistOff + i] = 0u;
-  if (bid == 0 && t == 0) rs[kCntOff] = 0u;
-  dbg_stamp(dbk, 12);
-}
-
 // A list bound that lists nothing; a row whose bound it is goes to the
-// histogram form (it cannot hold K keys >= the bound).
+// single-workgroup select (it cannot hold K keys >= the bound).
 constexpr uint32_t kNoKeys = 0xffffffffu;
 __device__ __forceinline__ uint32_t next_bin_key(uint32_t bin) { return bin >= 4095u ? kNoKeys : (bin + 1u) << 20; }
 
@@ -763,8 +562,9 @@ __device__ __forceinline__ uint32_t lane_rank(uint64_t m) {
 // alone, finds the exact K-th key t* of their union and the ties to take.
 // The union holds every key >= t* of the row when it holds at least K keys
 // >= L = the largest bound (then t* >= L); the workgroups check that (they
-// all see the same lists, so they agree) and otherwise hand the row to the
-// histogram form.  The offsets follow from the lists of the workgroups
+// all see the same lists, so they agree) and otherwise return false: the
+// caller then has the row selected by one workgroup over its scores in
+// memory (topk.hip finalize_row).  The offsets follow from the lists of the workgroups
 // before this one; each workgroup then writes its own selected positions
 // (KV slots) in position order.
 // Expects, from the scan: the own keys in cs.keys (position order), their
@@ -775,7 +575,7 @@ __device__ __forceinline__ uint32_t lane_rank(uint64_t m) {
 // past the union they read as 0, below every bound, so every per-entry loop
 // runs NU times without a guard.
 template <bool TOPK, int NU>
-__device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem, const ScanArgs& S, int bid,
+__device__ __forceinline__ bool coop_select(CoopShared& cs, unsigned char* smem, const ScanArgs& S, int bid,
                                             int nb, int len, int p_lo, int p_hi, uint32_t* rs,
                                             const float* srow, const int* pt_row, int* o, const int* pts,
                                             int pg0, bool pts_lds) {
@@ -846,9 +646,7 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
   dbg_value(dbk, 27, all ? 9ull : ((uint32_t)nown <= (uint32_t)P ? 3ull : (lo_b == 0u ? 4ull : ((lo_b & 0xfffffu) ? 2ull : 0ull))));
   // ---- publish in position order: thread t takes contiguous positions and
   // one block scan gives it its slots; the entries' positions stay in LDS
-  // (lpos, shared with the histogram form's candidates, which that form
-  // writes only after this one gave up) for the emit, then zero padding,
-  // header
+  // (lpos) for the emit, then zero padding, header
   uint16_t* lpos = cs.lpos;  // a list holds <= kPubWords entries
   {
     uint32_t* mine = gpub + (long)bid * P;
@@ -990,11 +788,7 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
       nbin = th.cnt;
     }
     dbg_stamp(dbk, 4);
-    if (!ok) {
-      dbg_stamp(dbk, 13);
-      coop_select_hist<TOPK>(cs, smem, S, bid, nb, len, p_lo, p_hi, rs, srow, pt_row, o);
-      return;
-    }
+    if (!ok) return false;  // every workgroup decides alike (the same lists)
     // pass 2: finite keys above T1's bin are selected: count them (and
     // those of the lists before this one; a list is a whole number of
     // uint4s); T1's bin -> candidates.  Edges: bin > T1 <=> w > top, and
@@ -1163,7 +957,7 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
     if (bid == nb - 1)
       for (int j = (int)nsel + t; j < K; j += kMainThreads) o[j] = TOPK ? S.pad : -1;
     dbg_stamp(dbk, 11);
-    return;
+    return true;
   }
   const int per = (n_e + kMainThreads - 1) / kMainThreads;
   const int e0 = min(n_e, t * per), e1 = min(n_e, e0 + per);
@@ -1209,6 +1003,7 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
   if (bid == nb - 1)
     for (int j = (int)nsel + t; j < K; j += kMainThreads) o[j] = TOPK ? S.pad : -1;
   dbg_stamp(dbk, 11);
+  return true;
 }
 
 template <int VARIANT>
@@ -1507,13 +1302,18 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
     CoopShared& cs = *reinterpret_cast<CoopShared*>(smem);
     int* o = S.next_idx + (long)row * S.topk;
     const int p_hi = min(c1 * kChunkKeys, len);
-    if (nb * pub_stride(nb, S.topk) <= 4 * 4 * kMainThreads)
-      coop_select<TOPK, 4>(cs, smem, S, bid, nb, len, c0 * kChunkKeys, p_hi, rs, srow, pt_row, o, sh.pts, pg0,
-                           pts_lds);
-    else
-      coop_select<TOPK, 8>(cs, smem, S, bid, nb, len, c0 * kChunkKeys, p_hi, rs, srow, pt_row, o, sh.pts, pg0,
-                           pts_lds);
-    return;
+    const bool decided =
+        nb * pub_stride(nb, S.topk) <= 4 * 4 * kMainThreads
+            ? coop_select<TOPK, 4>(cs, smem, S, bid, nb, len, c0 * kChunkKeys, p_hi, rs, srow, pt_row, o, sh.pts,
+                                   pg0, pts_lds)
+            : coop_select<TOPK, 8>(cs, smem, S, bid, nb, len, c0 * kChunkKeys, p_hi, rs, srow, pt_row, o, sh.pts,
+                                   pg0, pts_lds);
+    if (decided) return;
+    // The lists could not decide (e.g. many equal scores): the row is
+    // selected by one workgroup over its scores in memory, as without the
+    // cooperative select.  Its histogram is rebuilt from the own keys (the
+    // scan's one in LDS was reused by the union).
+    for (int i = t; i < p_hi - c0 * kChunkKeys; i += kMainThreads) atomicAdd(&rs[kHistOff + (cs.keys[i] >> 20)], 1u);
   }
   // arrival: wait for this slice's device-scope score stores and histogram
   // atomics, then count; the row's last slice selects
