@@ -1022,6 +1022,93 @@ __device__ __forceinline__ v4f qk_fp8(const v8i& qa, const v8i& kb) {
   return acc;
 }
 
+// The single-workgroup select of one row over its scores in memory: the
+// cooperative select's fallback (its lists could not decide, e.g. many equal
+// scores) and the select of rows the cooperative one does not take.  Exact
+// top-K by rank key, ties to the lower position, the same rule as
+// coop_select: t* by three radix passes over the row's keys (bits 31-21,
+// 20-10, 9-0; an LDS histogram each), then one pass in position order that
+// writes every finite key above t* and the lowest-position ties at t* (KV
+// slots through the page table; positions when TOPK has none), pads after.
+// It reads the row four times; compact on purpose (it shares the kernel's
+// registers with the common path).
+constexpr int kRowSelWords = 2048 + 4 * 8 + 4;  // LDS words select_row uses
+template <bool TOPK>
+__device__ __forceinline__ void select_row(unsigned char* smem, const float* srow, int len, const int* pt_row,
+                                           int* o, int K, int pad) {
+  uint32_t* hist = reinterpret_cast<uint32_t*>(smem);
+  uint32_t* wtmp = hist + 2048;
+  uint32_t* res = wtmp + 4 * 8;
+  const int t = threadIdx.x;
+  constexpr int kT = kMainThreads, kB = 8;  // loads in flight per thread
+  const __amdgpu_buffer_rsrc_t sr = dev_rsrc(srow, 4u * (uint32_t)max(len, 0));
+  uint32_t tstar = 0, need = 0;  // need: ties at t* to take
+  if (len > K) {
+    need = (uint32_t)K;
+    uint32_t prefix = 0;
+    for (int p = 0; p < 3; ++p) {
+      const int sh = p == 0 ? 21 : (p == 1 ? 10 : 0), bits = p == 2 ? 10 : 11;
+      for (int i = t; i < 2048; i += kT) hist[i] = 0u;
+      __syncthreads();
+      for (int i0 = 0; i0 < len; i0 += kB * kT) {
+        uint32_t k[kB];
+#pragma unroll
+        for (int j = 0; j < kB; ++j) {
+          const int i = i0 + j * kT + t;
+          k[j] = rank_key(__uint_as_float(load_dev4(sr, i < len ? 4u * (uint32_t)i : 0xfffffffcu)));
+        }
+#pragma unroll
+        for (int j = 0; j < kB; ++j)
+          if (i0 + j * kT + t < len && (p == 0 || (k[j] >> (sh + bits)) == prefix))
+            atomicAdd(&hist[(k[j] >> sh) & ((1u << bits) - 1u)], 1u);
+      }
+      __syncthreads();
+      find_threshold(hist, 1 << bits, need, wtmp, res);
+      prefix = (prefix << bits) | res[0];
+      need -= res[1];
+      __syncthreads();
+    }
+    tstar = prefix;
+  }
+  // position order: thread t takes positions [i0 + kB t, +kB) of each round
+  uint32_t run_sel = 0, run_tie = 0;
+  for (int i0 = 0; i0 < len; i0 += kB * kT) {
+    uint32_t k[kB];
+#pragma unroll
+    for (int j = 0; j < kB; ++j) {
+      const int i = i0 + kB * t + j;
+      k[j] = rank_key(__uint_as_float(load_dev4(sr, i < len ? 4u * (uint32_t)i : 0xfffffffcu)));
+    }
+    uint32_t nt = 0;
+#pragma unroll
+    for (int j = 0; j < kB; ++j) nt += (len > K && i0 + kB * t + j < len && k[j] == tstar) ? 1u : 0u;
+    uint32_t tie_tot;
+    uint32_t tr = run_tie + block_exclusive_scan(nt, wtmp, &tie_tot);
+    uint32_t ns = 0;
+    bool sel[kB];
+#pragma unroll
+    for (int j = 0; j < kB; ++j) {
+      const bool in = i0 + kB * t + j < len;
+      const bool tie = len > K && in && k[j] == tstar;
+      sel[j] = in && key_is_finite(k[j]) && (len <= K || k[j] > tstar || (tie && tr < need));
+      tr += tie ? 1u : 0u;
+      ns += sel[j] ? 1u : 0u;
+    }
+    uint32_t sel_tot;
+    uint32_t pos = run_sel + block_exclusive_scan(ns, wtmp, &sel_tot);
+#pragma unroll
+    for (int j = 0; j < kB; ++j)
+      if (sel[j]) {
+        const int i = i0 + kB * t + j;
+        o[min(pos++, (uint32_t)K - 1u)] =
+            (TOPK && !pt_row) ? i : pt_row[i >> 6] * DSA_PAGE_TOKENS + (i & (DSA_PAGE_TOKENS - 1));
+      }
+    run_sel += sel_tot;
+    run_tie += tie_tot;
+  }
+  for (int j = (int)run_sel + t; j < K; j += kT) o[j] = pad;
+}
+
 // Workgroup i's share [part(n, i, nb), part(n, i + 1, nb)) of n items, in
 // 32-bit unsigned arithmetic (a 64-bit division is ~100 instructions, and
 // every instruction on this serial path costs ~2 ns): n * nb < 2^32, which
@@ -1288,11 +1375,6 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   }
   dbg_stamp(dbk, 6);
   uint32_t* rs = S.hist + (long)row * S.hist_row_words;
-  if (!S.coop)
-    for (int i = t; i < kHistBins; i += kMainThreads) {
-      const uint32_t c = sh.hist[i];
-      if (c) atomicAdd(&rs[i], c);
-    }
   dbg_stamp(dbk, 3);
   if constexpr (!SELECT) return;
   if (!S.next_idx) return;
@@ -1309,14 +1391,12 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
             : coop_select<TOPK, 8>(cs, smem, S, bid, nb, len, c0 * kChunkKeys, p_hi, rs, srow, pt_row, o, sh.pts,
                                    pg0, pts_lds);
     if (decided) return;
-    // The lists could not decide (e.g. many equal scores): the row is
+    // the lists could not decide (e.g. many equal scores): the row is
     // selected by one workgroup over its scores in memory, as without the
-    // cooperative select.  Its histogram is rebuilt from the own keys (the
-    // scan's one in LDS was reused by the union).
-    for (int i = t; i < p_hi - c0 * kChunkKeys; i += kMainThreads) atomicAdd(&rs[kHistOff + (cs.keys[i] >> 20)], 1u);
+    // cooperative select
   }
-  // arrival: wait for this slice's device-scope score stores and histogram
-  // atomics, then count; the row's last slice selects
+  // arrival: wait for this slice's device-scope score stores, then count;
+  // the row's last slice selects
   wait_mem();
   __syncthreads();
   __shared__ uint32_t last;
@@ -1325,9 +1405,8 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   if (!last) return;
   if (t == 0) rs[kArrOff] = 0u;
   dbg_stamp(dbk, 4);
-  FinShared& fs = *reinterpret_cast<FinShared*>(smem);  // the scan's LDS is dead now
-  finalize_row(fs, srow, len, pt_row, S.pt_stride, rs, S.next_idx + (long)row * S.topk,
-               S.slab_stride, S.topk, /*sorted=*/0, TOPK ? S.pad : -1, /*fused=*/true);
+  __syncthreads();  // the scan's LDS is dead now
+  select_row<TOPK>(smem, srow, len, pt_row, S.next_idx + (long)row * S.topk, S.topk, TOPK ? S.pad : -1);
   dbg_stamp(dbk, 5);
 }
 
@@ -1543,7 +1622,7 @@ static hipError_t launch_nhg(dim3 grid, size_t lds, size_t lds_max, hipStream_t 
 hipError_t launch_decode_main(const AttnArgs* A, int B_att, const ScanArgs* S, int B_scan,
                               hipStream_t s) {
   const size_t lds_attn = sizeof(AttnShared);
-  const size_t lds_coop = std::max(sizeof(CoopShared), row_select_lds_bytes());
+  const size_t lds_coop = std::max(sizeof(CoopShared), (size_t)kRowSelWords * 4);
   const size_t lds_max = std::max(lds_attn, lds_coop);
   AttnArgs a{};
   ScanArgs sc{};
@@ -1595,7 +1674,7 @@ hipError_t launch_decode_main(const AttnArgs* A, int B_att, const ScanArgs* S, i
   if (n_att + n_scan == 0) return hipSuccess;
   size_t lds = sizeof(ScanShared);
   if (n_att) lds = std::max(lds, lds_attn);
-  if (select) lds = std::max(lds, sc.coop ? lds_coop : row_select_lds_bytes());
+  if (select) lds = std::max(lds, sc.coop ? lds_coop : (size_t)kRowSelWords * 4);
   const dim3 grid(n_att + n_scan);
   switch (S ? sc.Hidx / 16 : 4) {
     case 1: return launch_nhg<1>(grid, lds, lds_max, s, a, n_att, sc);
