@@ -144,24 +144,28 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
   // the first two tiles' slots before the query (the gathers depend on them)
   const int slot0 = key_slot(k0 + 16 * wv + kr);
   int slot_next = key_slot(k0 + kTile + 16 * wv + kr);
-  // this lane's bytes of one key row (zeros for an invalid slot)
+  // This lane's bytes of one key row (zeros for an invalid slot).  Step i
+  // of a row's 512 latent bytes: lane (kr, kc) reads bytes 64i + 16kc ..
+  // + 16 of key kr, so each load instruction reads 64 contiguous bytes of
+  // each of its 16 rows (a load whose 64 lanes touch 64 different cache
+  // lines is bound by the vector L1's line lookups, not by memory).  The
+  // dot product is over all dims, so the query takes the same dim order.
   struct RowRegs {
     uint4 nope[8], rope[2];
-    float sc;
+    float4 sc;  // the row's 4 scales (one per 128 dims)
     bool valid;
   };
   const auto load_row = [&](int slot, RowRegs& r) {
     r.valid = slot >= 0 && (long)slot < A.kv_rows;
-    r.sc = 0.f;
+    r.sc = make_float4(0.f, 0.f, 0.f, 0.f);
     if (r.valid) {
       const uint8_t* rowp = A.pool + (long)slot * DSA_LATENT_ROW_BYTES;
-      const uint4* np = reinterpret_cast<const uint4*>(rowp + 128 * kc);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) r.nope[i] = np[i];
-      r.sc = reinterpret_cast<const float*>(rowp + DSA_LATENT_DIM)[kc];
-      const uint4* rp = reinterpret_cast<const uint4*>(rowp + DSA_LATENT_DIM + 16 + 32 * kc);
-      r.rope[0] = rp[0];
-      r.rope[1] = rp[1];
+      for (int i = 0; i < 8; ++i) r.nope[i] = *reinterpret_cast<const uint4*>(rowp + 64 * i + 16 * kc);
+      r.sc = *reinterpret_cast<const float4*>(rowp + DSA_LATENT_DIM);
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+        r.rope[s2] = *reinterpret_cast<const uint4*>(rowp + DSA_LATENT_DIM + 16 + 64 * s2 + 16 * kc);
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) r.nope[i] = make_uint4(0, 0, 0, 0);
@@ -171,15 +175,20 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
   RowRegs cur;
   load_row(slot0, cur);
 
-  // Q (A operand): step s<16 -> dims 128kc + 8s; s = 16, 17 -> 512 + 16kc + 8(s-16)
+  // Q (A operand) in the keys' dim order: steps 2i, 2i + 1 -> dims 64i +
+  // 16kc + 0..7, + 8..15; steps 16 + s -> rope dims 32s + 8kc + 0..7.  A
+  // wave with no keys in its split (short splits) loads none.
   uint4 qa[18];
-  {
+  if (16 * wv < k1 - k0) {
     const uint16_t* qrow = A.q + ((long)b * A.H + hg * kHG + kr) * DSA_QK_DIM;
 #pragma unroll
-    for (int s = 0; s < 16; ++s) qa[s] = *reinterpret_cast<const uint4*>(qrow + 128 * kc + 8 * s);
+    for (int s = 0; s < 16; ++s) qa[s] = *reinterpret_cast<const uint4*>(qrow + 64 * (s >> 1) + 16 * kc + 8 * (s & 1));
 #pragma unroll
     for (int s = 0; s < 2; ++s)
-      qa[16 + s] = *reinterpret_cast<const uint4*>(qrow + DSA_LATENT_DIM + 16 * kc + 8 * s);
+      qa[16 + s] = *reinterpret_cast<const uint4*>(qrow + DSA_LATENT_DIM + 32 * s + 8 * kc);
+  } else {
+#pragma unroll
+    for (int s = 0; s < 18; ++s) qa[s] = make_uint4(0, 0, 0, 0);
   }
   if (t < kHG) { sh.m[t] = -INFINITY; sh.l[t] = 0.f; }
 
@@ -199,20 +208,20 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
     const bool valid = cur.valid;
     const uint4* nope = cur.nope;
     const uint4* rope = cur.rope;
-    const float sc = cur.sc;
+    const float sc4[4] = {cur.sc.x, cur.sc.y, cur.sc.z, cur.sc.w};
 
     // dequantise -> QK MFMA + row-major value tile (16-byte stores)
     const int kl = 16 * wv + kr;
-    uint4* vrow = reinterpret_cast<uint4*>(sh.vt + kl * kVLd + 128 * kc);
+    uint4* vrow = reinterpret_cast<uint4*>(sh.vt + kl * kVLd + 16 * kc);
     v4f sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       uint4 lo, hi;
-      dequant16(nope[i], sc, lo, hi);
+      dequant16(nope[i], sc4[i >> 1], lo, hi);
       sacc = mfma_bf16(qa[2 * i], lo, sacc);
       sacc = mfma_bf16(qa[2 * i + 1], hi, sacc);
-      vrow[2 * i] = lo;
-      vrow[2 * i + 1] = hi;
+      vrow[8 * i] = lo;  // dims 64i + 16kc ..
+      vrow[8 * i + 1] = hi;
     }
     sacc = mfma_bf16(qa[16], rope[0], sacc);
     sacc = mfma_bf16(qa[17], rope[1], sacc);
