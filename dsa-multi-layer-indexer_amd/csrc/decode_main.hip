@@ -326,15 +326,20 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
   }
 
   dbg_stamp(dbk, 3);
-  // partials: O [16][512] (unnormalised), (m, l) per head, log2 domain
+  // partials: O (unnormalised) in the MFMA's output layout, [512 dims][16
+  // heads]: lane (kr, kc) of n-tile nt holds heads 4kc .. 4kc + 3 of dim
+  // 64wv + 16nt + kr, one 16-byte store, so each wave store writes 1 KB
+  // contiguous (16 dims x 16 heads; per-element stores of a [head][dim]
+  // layout took ~0.8 us to issue).  (m, l) per head, log2 domain.
   const long pblk0 = ((long)b * nhg + hg) * nsplit;
   const long pblk = pblk0 + sp;
-  float* po = A.part_o + pblk * (kHG * DSA_LATENT_DIM);
+  {
+    const __amdgpu_buffer_rsrc_t pw = dev_rsrc(A.part_o + pblk * (kHG * DSA_LATENT_DIM), kHG * DSA_LATENT_DIM * 4u);
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      store_dev(&po[(4 * kc + r) * DSA_LATENT_DIM + 64 * wv + 16 * nt + kr], o[nt][r]);
+    for (int nt = 0; nt < 4; ++nt)
+      store_dev16(pw, 4u * (uint32_t)((64 * wv + 16 * nt + kr) * kHG + 4 * kc),
+                  make_float4(o[nt][0], o[nt][1], o[nt][2], o[nt][3]));
+  }
   if (t < kHG) {
     store_dev(&A.part_ml[pblk * (2 * kHG) + 2 * t], sh.m[t]);
     store_dev(&A.part_ml[pblk * (2 * kHG) + 2 * t + 1], sh.l[t]);
@@ -348,7 +353,9 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
   // log-sum-exp merge (reference combine_kernel K:996-1045):
   // m* = max m_s, L = sum l_s 2^(m_s - m*), out = sum O_s 2^(m_s - m*) / L,
   // the splits summed in a fixed order (deterministic output).
-  constexpr int kVec = kHG * DSA_LATENT_DIM / 4;  // float4 outputs of the group
+  // float4 units of the group's outputs: unit v = heads 4(v & 3) .. + 3 of
+  // dim v >> 2 (the partials' layout)
+  constexpr int kVec = kHG * DSA_LATENT_DIM / 4;
   float* mls = reinterpret_cast<float*>(sh.vt);
   float* wgt = mls + kMaxSplit * 2 * kHG;
   float4* red = reinterpret_cast<float4*>(wgt + kMaxSplit * kHG);
@@ -397,8 +404,10 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
 #pragma unroll
     for (int j = 0; j < kPerLane; ++j) {
       const int s2 = i + 16 * j;
-      ms[j] = s2 < nsplit ? mls[s2 * 2 * kHG + 2 * h] : -INFINITY;
-      ls[j] = s2 < nsplit ? mls[s2 * 2 * kHG + 2 * h + 1] : 0.f;
+      const float2 ml = s2 < nsplit ? *reinterpret_cast<const float2*>(&mls[s2 * 2 * kHG + 2 * h])
+                                    : make_float2(-INFINITY, 0.f);
+      ms[j] = ml.x;
+      ls[j] = ml.y;
       mx = fmaxf(mx, ms[j]);
     }
     mx = row16_reduce<2>(mx);
@@ -424,15 +433,16 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     if (active) {
       const int v = v_lo + vi;
-      const int h = v / (DSA_LATENT_DIM / 4);
+      const int h0 = 4 * (v & 3);
       const int s0 = g * spg, s1 = min(nsplit, s0 + spg);
       for (int sb = s0; sb < s1; sb += kLd) {
         if (r0 != 0 || sb != s0) load_x(v, sb, s1);
 #pragma unroll
         for (int i = 0; i < kLd; ++i) {
-          const float wt = (sb + i < s1) ? wgt[(sb + i) * kHG + h] : 0.f;
-          acc.x += x[i].x * wt; acc.y += x[i].y * wt;
-          acc.z += x[i].z * wt; acc.w += x[i].w * wt;
+          const float4 wt = (sb + i < s1) ? *reinterpret_cast<const float4*>(&wgt[(sb + i) * kHG + h0])
+                                          : make_float4(0.f, 0.f, 0.f, 0.f);
+          acc.x += x[i].x * wt.x; acc.y += x[i].y * wt.y;
+          acc.z += x[i].z * wt.z; acc.w += x[i].w * wt.w;
         }
       }
     }
@@ -448,12 +458,12 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
     }
     if (g == 0 && active) {
       const int v = v_lo + vi;
-      const int h = v / (DSA_LATENT_DIM / 4);
-      uint2 pk;
-      pk.x = pack_bf16x2(acc.x, acc.y);
-      pk.y = pack_bf16x2(acc.z, acc.w);
-      const int d = (v % (DSA_LATENT_DIM / 4)) * 4;
-      *reinterpret_cast<uint2*>(A.out + ((long)b * A.H + hg * kHG + h) * DSA_LATENT_DIM + d) = pk;
+      const uint32_t p01 = pack_bf16x2(acc.x, acc.y), p23 = pack_bf16x2(acc.z, acc.w);
+      uint16_t* op = A.out + ((long)b * A.H + hg * kHG + 4 * (v & 3)) * DSA_LATENT_DIM + (v >> 2);
+      op[0] = (uint16_t)p01;
+      op[DSA_LATENT_DIM] = (uint16_t)(p01 >> 16);
+      op[2 * DSA_LATENT_DIM] = (uint16_t)p23;
+      op[3 * DSA_LATENT_DIM] = (uint16_t)(p23 >> 16);
     }
   }
   dbg_stamp(dbk, 7);

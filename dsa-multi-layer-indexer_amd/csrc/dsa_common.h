@@ -223,6 +223,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const void* base, uin
 __device__ __forceinline__ uint4 load_dev16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCpolSc1));
 }
+// 16-byte device-scope store at byte offset off (dropped beyond the size)
+__device__ __forceinline__ void store_dev16(__amdgpu_buffer_rsrc_t r, uint32_t off, float4 v) {
+  typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), r, off, 0, kCpolSc1);
+}
 __device__ __forceinline__ uint32_t load_dev4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kCpolSc1);
 }
