@@ -247,21 +247,31 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
     const uint4* rope = cur.rope;
     const float sc4[4] = {cur.sc.x, cur.sc.y, cur.sc.z, cur.sc.w};
 
-    // dequantise -> QK MFMA + row-major value tile (16-byte stores)
+    // dequantise -> QK MFMA + row-major value tile (16-byte stores).  The
+    // dequant is VALU-bound and a SIMD runs two waves, so a wave with no key
+    // in this tile skips it (zeroing its value rows when the PV k-steps in
+    // use cover them); the PV below skips k-steps past the tile's keys.
+    const int nk = k1 - tile0;                        // keys in this tile
+    const int nks = min(kTile / 32, (nk + 31) >> 5);  // PV k-steps in use
     const int kl = 16 * wv + kr;
     uint4* vrow = reinterpret_cast<uint4*>(sh.vt + kl * kVLd + 16 * kc);
     v4f sacc = {0.f, 0.f, 0.f, 0.f};
+    if (16 * wv < nk) {  // uniform
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      uint4 lo, hi;
-      dequant16(nope[i], sc4[i >> 1], lo, hi);
-      sacc = mfma_bf16(qa[2 * i], lo, sacc);
-      sacc = mfma_bf16(qa[2 * i + 1], hi, sacc);
-      vrow[8 * i] = lo;  // dims 64i + 16kc ..
-      vrow[8 * i + 1] = hi;
+      for (int i = 0; i < 8; ++i) {
+        uint4 lo, hi;
+        dequant16(nope[i], sc4[i >> 1], lo, hi);
+        sacc = mfma_bf16(qa[2 * i], lo, sacc);
+        sacc = mfma_bf16(qa[2 * i + 1], hi, sacc);
+        vrow[8 * i] = lo;  // dims 64i + 16kc ..
+        vrow[8 * i + 1] = hi;
+      }
+      sacc = mfma_bf16(qa[16], rope[0], sacc);
+      sacc = mfma_bf16(qa[17], rope[1], sacc);
+    } else if (16 * wv < 32 * nks) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) vrow[8 * i] = vrow[8 * i + 1] = make_uint4(0, 0, 0, 0);
     }
-    sacc = mfma_bf16(qa[16], rope[0], sacc);
-    sacc = mfma_bf16(qa[17], rope[1], sacc);
     dbg_stamp(dbk, 1);
     // lane holds key kl (column), heads 4kc + r (rows)
 #pragma unroll
@@ -314,6 +324,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
       for (int r = 0; r < 4; ++r) o[nt][r] *= a4[r];
 #pragma unroll
     for (int ks = 0; ks < kTile / 32; ++ks) {
+      if (ks >= nks) break;  // uniform: no keys past here
       const uint4 pa = *reinterpret_cast<const uint4*>(sh.p + kr * kPLd + 32 * ks + 8 * kc);
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) {
