@@ -381,21 +381,24 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
   const int g = t / span;
   constexpr int kLd = 8;                   // partial loads in flight per thread
   float4 x[kLd];
-  // every load is issued (an unused one reads past the resource: 0), so
-  // the compiler can wait for each batch by count
+  // loads past s1 are not issued (s0, s1 are uniform over a wave: its
+  // threads form one group)
   auto load_x = [&](int v, int s0, int s1) {
 #pragma unroll
     for (int i = 0; i < kLd; ++i)
-      x[i] = __builtin_bit_cast(float4, load_dev16(prs, s0 + i < s1 ? 16u * ((s0 + i) * kVec + v) : 0xfffffff0u));
+      x[i] = s0 + i < s1 ? __builtin_bit_cast(float4, load_dev16(prs, 16u * ((s0 + i) * kVec + v)))
+                         : make_float4(0.f, 0.f, 0.f, 0.f);
   };
   {  // the splits' (m, l) first (nsplit*32 floats, <= 8 per thread), then this
      // thread's partials: the merge weights are computed while those arrive
     constexpr int kPer = kMaxSplit * 2 * kHG / kMainThreads;
     float v[kPer];
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) {
+    for (int j = 0; j < kPer; ++j) {  // rounds past the splits' pairs are skipped (uniform)
       const int i = t + j * kMainThreads;
-      v[j] = __uint_as_float(load_dev4(mrs, i < nsplit * 2 * kHG ? 4u * i : 0xfffffffcu));
+      v[j] = j * kMainThreads < nsplit * 2 * kHG
+                 ? __uint_as_float(load_dev4(mrs, i < nsplit * 2 * kHG ? 4u * i : 0xfffffffcu))
+                 : 0.f;
     }
     const bool act = g < G && t - g * span < nv;
     load_x(v_lo + t - g * span, act ? g * spg : 0, act ? min(nsplit, (g + 1) * spg) : 0);
