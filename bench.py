@@ -474,7 +474,14 @@ def main() -> int:
                 "serial_ms": round(t_attn + t_idx, 5),
                 "eager_layer_calls_ms": round(t_serial, 5), "attn_only_ms": round(t_attn, 5),
                 "indexer_only_ms": round(t_idx, 5),
-                "hidden_fraction": None if hidden is None else round(hidden, 4)},
+                "hidden_fraction": None if hidden is None else round(hidden, 4),
+                # the largest hidden fraction possible: the indexer can only
+                # hide under the attention's own time, so with the attention
+                # the shorter of the two the bound is t_attn / t_idx
+                "hidden_bound": None if t_idx <= 0 else round(min(1.0, t_attn / t_idx), 4),
+                # the other side: the share of the attention's time the step
+                # does not add on top of the indexer alone
+                "attention_hidden_fraction": None if t_attn <= 0 else round(1.0 - (t_full - t_idx) / t_attn, 4)},
         "roofline": {"bound": "hbm", "achieved": round(layer_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(layer_gbs / HBM_PEAK_GBS, 4),
                      "traffic": read_traffic() if args.config == "c3" else None,
