@@ -1210,6 +1210,14 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   const int sc0 = part(ncap, bid, nb), sc1 = part(ncap, bid + 1, nb);
   const int spg0 = sc0 >> 2;
   const int snpg = (sc1 > sc0) ? ((sc1 - 1) >> 2) - spg0 + 1 : 0;
+  // the row barriers' flag values (flipped once per use), loaded first and
+  // stored to LDS in this prologue: held in a register until the select, the
+  // load made the scan's end wait for every load and store the scan issued
+  // (the wait counter counts in issue order, stores included)
+  uint32_t sense = 0;
+  if (S.coop && t < kNumSync)
+    sense = group_sense(S.hist + (long)row * S.hist_row_words + row_sync_off(S.slab_stride) + t * kSyncWords,
+                        bid);
   constexpr int kQ = FROM_SCORES ? 0 : kHeads * DSA_INDEX_DIM / 16;  // uint4 of the query block
   const uint4* qsrc = reinterpret_cast<const uint4*>(S.q8 + (long)row * kHeads * DSA_INDEX_DIM);
   uint4 qv = make_uint4(0, 0, 0, 0);
@@ -1240,13 +1248,8 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
     }
     if (with_hist)
       for (int i = t; i < kHistWords / 4; i += kMainThreads) reinterpret_cast<uint4*>(sh.hist)[i] = make_uint4(0, 0, 0, 0);
+    if (S.coop && t < kNumSync) reinterpret_cast<CoopShared*>(smem)->sense[t] = sense;
   }
-  // the row barriers' flag values (flipped once per use), read now and
-  // stored for the select after the scan (the loads' latency hides under it)
-  uint32_t sense = 0;
-  if (S.coop && t < kNumSync)
-    sense = group_sense(S.hist + (long)row * S.hist_row_words + row_sync_off(S.slab_stride) + t * kSyncWords,
-                        bid);
   float* srow = S.scores + (long)row * S.slab_stride;
   if constexpr (!FROM_SCORES) {  // slab tail past the last scored chunk -> -inf, over the row's blocks
     const long tail0 = (long)nchunks * kChunkKeys;
@@ -1419,7 +1422,6 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   if constexpr (SELECT) {
     if (S.coop) {
       CoopShared& cs = *reinterpret_cast<CoopShared*>(smem);
-      if (t < kNumSync) cs.sense[t] = sense;
       kmax = wave_reduce<2>(kmax);
       nfin = wave_reduce<0>(nfin);
       if (lane == 0) {
@@ -1427,8 +1429,6 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
         cs.wstat[2 * wv + 1] = kmax;
       }
     }
-  } else {
-    if (S.coop && t < kNumSync) reinterpret_cast<CoopShared*>(smem)->sense[t] = sense;
   }
   __syncthreads();
   if constexpr (FROM_SCORES && SELECT) {
