@@ -1375,7 +1375,11 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
           for (int hg = 0; hg < NHG; ++hg) {
             const v4f d = qk_fp8<VARIANT>(qa[hg], kb);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) a[j] += wr[hg][r] * fmaxf(d[r], 0.f);
+            // ReLU as one integer max on the bits (a negative float, -0
+            // included, is a negative integer): fmaxf adds a NaN-quieting
+            // max before each, and the MFMA of finite fp8 values is finite
+            for (int r = 0; r < 4; ++r)
+              a[j] += wr[hg][r] * __int_as_float(max(__float_as_int(d[r]), 0));
           }
         }
         // permlane32_swap(x, y) -> {[x.lo, y.lo], [x.hi, y.hi]} (32-lane
