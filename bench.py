@@ -391,8 +391,14 @@ def main() -> int:
     t_idx = time_graph(rotated(idx_onlys), reps, torch)
     t_full = time_graph(rotated(fulls), reps, torch)
     hidden = 1.0 - (t_full - t_attn) / t_idx if t_idx > 0 else None
-    # the same schedule without a graph, and layer by layer (one set, cache-warm)
-    t_eager = time_graph(lambda: fulls[0].run_eager(), reps, torch)
+    # the same schedule without a graph, over the same rotated sets
+    eager_state = {"i": 0}
+
+    def eager_rotated():
+        fulls[eager_state["i"] % len(fulls)].run_eager()
+        eager_state["i"] += 1
+    t_eager = time_graph(eager_rotated, reps, torch)
+    # and layer by layer (one set, cache-warm)
 
     def serial():
         att = first
