@@ -1190,7 +1190,9 @@ __device__ __forceinline__ int part(int n, int i, int nb) {
 // FROM_SCORES: the row's scores are already in the slab (a plain scan
 // launch wrote them); the workgroup loads its positions' scores instead of
 // scoring the keys, then selects as usual.
-template <int NHG, int VARIANT, bool SELECT, bool FROM_SCORES = false, bool TOPK = false>
+// LISTS: the cooperative select's union registers, 4 or 8 uint4s per thread
+// when the launch fixes one size for every row, 0 for both (chosen per row)
+template <int NHG, int VARIANT, bool SELECT, bool FROM_SCORES = false, bool TOPK = false, int LISTS = 0>
 __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, int nb, unsigned char* smem) {
   constexpr int kHeads = NHG * 16;
   ScanShared& sh = *reinterpret_cast<ScanShared*>(smem);
@@ -1454,16 +1456,26 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   if (!S.next_idx) return;
   if (S.coop) {
     // the union's uint4s per thread: 4 (up to 8192 entries, C3's 224 lists)
-    // or 8, each its own instantiation
+    // or 8.  A launch whose rows all have one size carries only that form
+    // (the other, unused, made the kernel's code larger; LISTS == 4 with a
+    // row of wider lists, which the launcher does not send, takes the
+    // single-workgroup select)
     CoopShared& cs = *reinterpret_cast<CoopShared*>(smem);
     int* o = S.next_idx + (long)row * S.topk;
     const int p_hi = min(c1 * kChunkKeys, len);
-    const bool decided =
-        nb * pub_stride(nb, S.topk) <= 4 * 4 * kMainThreads
-            ? coop_select<TOPK, 4>(cs, smem, S, bid, nb, len, c0 * kChunkKeys, p_hi, rs, srow, pt_row, o, sh.pts,
-                                   pg0, pts_lds)
-            : coop_select<TOPK, 8>(cs, smem, S, bid, nb, len, c0 * kChunkKeys, p_hi, rs, srow, pt_row, o, sh.pts,
-                                   pg0, pts_lds);
+    const bool narrow = nb * pub_stride(nb, S.topk) <= 4 * 4 * kMainThreads;
+    bool decided;
+    if constexpr (LISTS == 4)
+      decided = narrow && coop_select<TOPK, 4>(cs, smem, S, bid, nb, len, c0 * kChunkKeys, p_hi, rs, srow, pt_row,
+                                               o, sh.pts, pg0, pts_lds);
+    else if constexpr (LISTS == 8)
+      decided = coop_select<TOPK, 8>(cs, smem, S, bid, nb, len, c0 * kChunkKeys, p_hi, rs, srow, pt_row, o,
+                                     sh.pts, pg0, pts_lds);
+    else
+      decided = narrow ? coop_select<TOPK, 4>(cs, smem, S, bid, nb, len, c0 * kChunkKeys, p_hi, rs, srow, pt_row,
+                                              o, sh.pts, pg0, pts_lds)
+                       : coop_select<TOPK, 8>(cs, smem, S, bid, nb, len, c0 * kChunkKeys, p_hi, rs, srow, pt_row,
+                                              o, sh.pts, pg0, pts_lds);
     if (decided) return;
     // the lists could not decide (e.g. many equal scores): the row is
     // selected by one workgroup over its scores in memory, as without the
@@ -1496,8 +1508,10 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
 // kRoleFromScores: the select loads the scores a plain scan launch wrote
 // kRoleTopk: with kRoleFromScores, the standalone top-k (caller's pad value;
 //   positions when there is no page table)
+// kRoleWide: the select's lists of every row need 8 union uint4s per thread
+// (otherwise 4; planned launches choose per row)
 constexpr int kRoleAttn = 1, kRoleScan = 2, kRoleSelect = 4, kRolePlan = 8, kRoleFromScores = 16,
-              kRoleTopk = 32;
+              kRoleTopk = 32, kRoleWide = 64;
 
 // Workgroups per row by length (ragged batches of <= 64 rows): every row
 // gets the workgroups its keys and page entries need (the cooperative
@@ -1566,8 +1580,9 @@ __global__ __launch_bounds__(kMainThreads, (ROLES & ~kRolePlan) == kRoleScan ? 4
       bid = slot.y;
       nb = slot.z;
     }
-    scan_block<NHG, VARIANT, (ROLES & kRoleSelect) != 0, (ROLES & kRoleFromScores) != 0, (ROLES & kRoleTopk) != 0>(
-        S, row, bid, nb, smem);
+    constexpr int kLists = (ROLES & kRolePlan) ? 0 : ((ROLES & kRoleWide) ? 8 : 4);
+    scan_block<NHG, VARIANT, (ROLES & kRoleSelect) != 0, (ROLES & kRoleFromScores) != 0, (ROLES & kRoleTopk) != 0,
+               kLists>(S, row, bid, nb, smem);
     dbg_flush(blockIdx.x);
   }
 }
@@ -1678,8 +1693,8 @@ static hipError_t launch_nhg_p(dim3 grid, size_t lds, size_t lds_max, hipStream_
                                                                                          n_att, S);
   }
   if (!att && !S.next_idx)  // plain scan: the only role with the alternative MFMA form
-    return g_scan_variant == 0 ? launch_k<NHG, 0, kRoleScan | PLAN>(grid, lds, lds_max, s, A, n_att, S)
-                               : launch_k<NHG, 1, kRoleScan | PLAN>(grid, lds, lds_max, s, A, n_att, S);
+    return g_scan_variant == 0 ? launch_k<NHG, 0, kRoleScan | (PLAN & kRolePlan)>(grid, lds, lds_max, s, A, n_att, S)
+                               : launch_k<NHG, 1, kRoleScan | (PLAN & kRolePlan)>(grid, lds, lds_max, s, A, n_att, S);
   if (!att) return launch_k<NHG, 0, kRoleScan | kRoleSelect | PLAN>(grid, lds, lds_max, s, A, n_att, S);
   return launch_k<NHG, 0, kRoleAttn | kRoleScan | kRoleSelect | PLAN>(grid, lds, lds_max, s, A, n_att, S);
 }
@@ -1689,8 +1704,12 @@ static hipError_t launch_nhg(dim3 grid, size_t lds, size_t lds_max, hipStream_t 
                              int n_att, const ScanArgs& S) {
   const bool scan = S.blocks_per_row > 0 && grid.x > (unsigned)n_att;
   if (!scan) return launch_k<4, 0, kRoleAttn>(grid, lds, lds_max, s, A, n_att, S);
-  return S.balance ? launch_nhg_p<NHG, kRolePlan>(grid, lds, lds_max, s, A, n_att, S)
-                   : launch_nhg_p<NHG, 0>(grid, lds, lds_max, s, A, n_att, S);
+  if (S.balance) return launch_nhg_p<NHG, kRolePlan>(grid, lds, lds_max, s, A, n_att, S);
+  // one workgroup count for every row: the select's union size is fixed
+  const bool wide = S.next_idx && S.coop &&
+                    (long)S.blocks_per_row * pub_stride(S.blocks_per_row, S.topk) > 4L * 4 * kMainThreads;
+  return wide ? launch_nhg_p<NHG, kRoleWide>(grid, lds, lds_max, s, A, n_att, S)
+              : launch_nhg_p<NHG, 0>(grid, lds, lds_max, s, A, n_att, S);
 }
 
 hipError_t launch_decode_main(const AttnArgs* A, int B_att, const ScanArgs* S, int B_scan,
