@@ -145,6 +145,19 @@ def test_topk_position_order_large_k_and_lengths_past_slab(dev, k):
     _check(s, [40000, 90000, 8192, 39999, -3], k, False, dev, pad=-5)
 
 
+@pytest.mark.parametrize("k", [4096, 8192])
+def test_topk_position_order_one_row_wide_lists(dev, k):
+    """One long row with a large k: every workgroup of the launch holds a
+    list too long for the 4-uint4 union, so the launch carries only the
+    8-uint4 form of the cooperative select; ties at the threshold too."""
+    rng = np.random.default_rng(29 + k)
+    print(f"[topk] one row k={k}", flush=True)
+    s = rng.standard_normal((1, 131072)).astype(np.float32)
+    _check(s, [131072], k, False, dev)
+    s[0] = np.round(s[0] * 8) / 8
+    _check(s, [131072], k, False, dev)
+
+
 @pytest.mark.parametrize("B", [64, 65, 300])
 def test_topk_position_order_many_rows(dev, B):
     """64 rows (per-row workgroup plan), 65 and 300 rows (uniform split)."""
