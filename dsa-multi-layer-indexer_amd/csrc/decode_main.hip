@@ -523,7 +523,7 @@ constexpr int kPubHdr = 4;           // list header: count, bound key, finite co
 constexpr int kCoopCand = 1024;      // threshold-bin candidates resolved by rank counting
 struct CoopShared {
   ScanShared scan;
-  uint32_t keys[kCoopKeys];
+  alignas(16) uint32_t keys[kCoopKeys];
   uint16_t lpos[kPubWords];  // the published entries: own position index
   uint32_t wave_tmp[4 * kMainWaves];
   uint32_t res[4];
@@ -692,9 +692,14 @@ __device__ __forceinline__ bool coop_select(CoopShared& cs, unsigned char* smem,
       uint32_t* sub = cs.ck;  // 256 counters; the candidates come later
       if (t < 256) sub[t] = 0u;
       __syncthreads();
-      for (int i = t; i < nown; i += kMainThreads) {
-        const uint32_t k = cs.keys[i];
-        if ((k >> 20) == th.bin) atomicAdd(&sub[(k >> 12) & 255u], 1u);
+      // four keys' loads in flight before their counts
+      for (int i = t; i < nown; i += 4 * kMainThreads) {
+        uint32_t kk[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) kk[u] = i + u * kMainThreads < nown ? cs.keys[i + u * kMainThreads] : 0u;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (i + u * kMainThreads < nown && (kk[u] >> 20) == th.bin) atomicAdd(&sub[(kk[u] >> 12) & 255u], 1u);
       }
       __syncthreads();
       // lane l: sub-bins 255-4l .. 252-4l, top down
@@ -714,13 +719,14 @@ __device__ __forceinline__ bool coop_select(CoopShared& cs, unsigned char* smem,
 
   dbg_stamp(dbk, 25);
   dbg_value(dbk, 27, all ? 9ull : ((uint32_t)nown <= (uint32_t)P ? 3ull : (lo_b == 0u ? 4ull : ((lo_b & 0xfffffu) ? 2ull : 0ull))));
-  // ---- publish in position order: thread t takes contiguous positions and
-  // one block scan gives it its slots; the entries' positions stay in LDS
+  // ---- publish in position order; the entries' positions stay in LDS
   // (lpos) for the emit, then zero padding, header
   uint16_t* lpos = cs.lpos;  // a list holds <= kPubWords entries
   {
     uint32_t* mine = gpub + (long)bid * P;
-    if (!all && lo_b != kNoKeys) {
+    if (!all && lo_b != kNoKeys && nown <= 4 * kMainThreads) {
+      // a few positions per thread: thread t takes contiguous positions and
+      // one block scan gives it its slots
       const int per = (nown + kMainThreads - 1) / kMainThreads;
       const int i0 = min(nown, t * per), i1 = min(nown, i0 + per);
       uint32_t c = 0;
@@ -736,6 +742,61 @@ __device__ __forceinline__ bool coop_select(CoopShared& cs, unsigned char* smem,
           lpos[slot] = (uint16_t)i;
           store_dev(&mine[slot], k);
         }
+      }
+    } else if (!all && lo_b != kNoKeys) {
+      // many positions: wave w takes the contiguous positions [w * seg,
+      // (w + 1) * seg) in steps of 256 (lane l: positions 4l .. 4l + 3 of
+      // the step, one 16-byte LDS read; every step's read issued at once),
+      // orders its entries by lane within a step (a wave scan) and places
+      // them after those of the waves before it.  (Thread-contiguous runs of
+      // this length cost one dependent LDS round trip per position.)
+      constexpr int kStep = 4 * kWave, kSteps = kCoopKeys / (kMainWaves * kStep);
+      static_assert(kSteps * kMainWaves * kStep == kCoopKeys, "publish steps cover the own keys");
+      const int seg = (nown + kMainWaves * kStep - 1) / (kMainWaves * kStep) * kStep;
+      const int w0 = min(nown, wv * seg), w1 = min(nown, w0 + seg);  // wave-uniform
+      const uint4* k4 = reinterpret_cast<const uint4*>(cs.keys);
+      uint4 kv[kSteps];
+      uint32_t sel[kSteps];  // bit e: position 4 * lane + e of the step is listed
+#pragma unroll
+      for (int st = 0; st < kSteps; ++st) {
+        const int i = w0 + st * kStep + 4 * lane;
+        kv[st] = k4[(i < kCoopKeys ? i : 0) >> 2];  // in bounds; masked below
+      }
+      uint32_t c = 0;
+#pragma unroll
+      for (int st = 0; st < kSteps; ++st) {
+        const int i = w0 + st * kStep + 4 * lane;
+        const uint32_t w4[4] = {kv[st].x, kv[st].y, kv[st].z, kv[st].w};
+        uint32_t m = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) m |= (i + e < w1 && w4[e] >= lo_b) ? 1u << e : 0u;
+        sel[st] = m;
+        c += (uint32_t)__popc(m);
+      }
+      c = wave_reduce<0>(c);
+      // no closing barrier: wave_tmp is next written after the group barrier
+      if (lane == 0) cs.wave_tmp[wv] = c;
+      __syncthreads();
+      uint32_t off = 0;
+#pragma unroll
+      for (int w = 0; w < kMainWaves; ++w) off += w < wv ? cs.wave_tmp[w] : 0u;
+      dbg_stamp(dbk, 26);
+#pragma unroll
+      for (int st = 0; st < kSteps; ++st) {
+        if (w0 + st * kStep >= w1) break;  // uniform
+        const uint32_t n = (uint32_t)__popc(sel[st]);
+        const uint32_t incl = wave_scan_incl<0>(n);
+        uint32_t slot = off + incl - n;
+        const int i = w0 + st * kStep + 4 * lane;
+        const uint32_t w4[4] = {kv[st].x, kv[st].y, kv[st].z, kv[st].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (sel[st] & (1u << e)) {
+            const uint32_t sl = min(slot++, (uint32_t)P - 1u);  // < cnt <= P by construction
+            lpos[sl] = (uint16_t)(i + e);
+            store_dev(&mine[sl], w4[e]);
+          }
+        off += (uint32_t)__builtin_amdgcn_readlane((int)incl, kWave - 1);
       }
     }
     if (!all)
