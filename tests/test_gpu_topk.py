@@ -202,3 +202,21 @@ def test_topk_position_order_rounded_scores_long_rows(dev, step):
     pt = np.stack([rng.permutation(4096)[:2048] for _ in range(3)]).astype(np.int32)
     _check(s, [131072, 100000, 65536], 2048, False, dev)
     _check(s, [131072, 100000, 65536], 2048, False, dev, pt=pt)
+
+
+@pytest.mark.parametrize("k", [1000, 2000])
+@pytest.mark.parametrize("ties", [False, True])
+def test_topk_position_order_list_publish_forms(dev, k, ties):
+    """More rows than the per-row workgroup plan takes (64), so every row
+    has one workgroup and its own-key count is the row length: lengths that
+    straddle the switch between the two list-publish forms (per-thread runs
+    up to 2048 own keys, wave segments above), with and without ties at the
+    threshold."""
+    rng = np.random.default_rng(41 + k + ties)
+    print(f"[topk] publish forms k={k} ties={ties}", flush=True)
+    base = [2047, 2048, 2049, 2050, 2303, 4097, 9001, 16384]
+    lens = (base * 38)[:300]
+    s = rng.standard_normal((len(lens), 16384)).astype(np.float32)
+    if ties:
+        s = np.round(s * 4) / 4
+    _check(s, lens, k, False, dev)
