@@ -41,6 +41,13 @@ def _layer(dev, lens, seed, pattern=None):
     elif pattern == "equal":  # every key and scale identical: all scores equal
         pages[:, :8192] = pages[0, :128].repeat(64)
         pages[:, 8192:].view(torch.float32).fill_(1.0)
+    elif pattern == "window":  # a 3000-token window of each row scores far above the rest
+        scales = pages[:, 8192:].view(torch.float32)  # [page][token in page]
+        ptc = pt.cpu().numpy()
+        for r, n in enumerate(lens):
+            a = n // 3
+            for pos in range(a, min(n, a + 3000)):
+                scales[int(ptc[r, pos // 64]), pos % 64] *= 50.0
     return L, pt
 
 
@@ -73,6 +80,12 @@ CASES = [
     # bins and sub-bins
     ([131072], 11, "dup"),
     ([131072, 70000], 12, "dup64"),
+    # the selected keys packed into one window of each row (a recent-token
+    # window): the workgroups over it hold more than their lists carry, so
+    # the cooperative select must find that and fall back
+    ([131072], 13, "window"),
+    ([131072, 70000, 9000], 14, "window"),
+    ([20000] * 9, 15, "window"),
 ]
 
 

@@ -220,3 +220,20 @@ def test_topk_position_order_list_publish_forms(dev, k, ties):
     if ties:
         s = np.round(s * 4) / 4
     _check(s, lens, k, False, dev)
+
+
+@pytest.mark.parametrize("sorted_", [False, True])
+def test_topk_top_keys_packed_in_one_window(dev, sorted_):
+    """The largest scores packed into one contiguous window of positions (a
+    recent-token window), distinct values: the workgroup over the window
+    holds far more selected keys than its list can carry, so the row must
+    be resolved by the single-workgroup fallback; the window also straddles
+    two workgroups' ranges and sits at the row's end."""
+    rng = np.random.default_rng(77)
+    print(f"[topk] packed window sorted={sorted_}", flush=True)
+    lens = [131072, 131072, 100000]
+    s = rng.standard_normal((3, 131072)).astype(np.float32)
+    s[0, 50000:54000] += 10.0                          # one window
+    s[1, 16384 - 1500:16384 + 1500] += 10.0            # straddles a workgroup edge
+    s[2, 100000 - 3000:100000] += 10.0                 # the row's last positions
+    _check(s, lens, 2048, sorted_, dev)
