@@ -186,6 +186,10 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--nsplit", type=int, default=0,
                     help="attention splits per (row, head group); 0 = the library's choice")
+    ap.add_argument("--scores", choices=["uniform", "window"], default="uniform",
+                    help="window: the keys of a 3000-token window of each row (from position len/3) "
+                         "score 50x the rest, so each row's top-2048 is packed in a few positions "
+                         "(a recent-token-heavy selection)")
     ap.add_argument("--max-sets", type=int, default=64,
                     help="cap on the rotated layer sets (1: no Infinity-Cache defeat)")
     ap.add_argument("--profile", choices=["fused", "scan", "topk", "attn", "two_stream"], default=None,
@@ -240,6 +244,19 @@ def main() -> int:
                                       nsplit=args.nsplit)
                   for i in range(n_layers)]
         sets.append(layers)
+    if args.scores == "window":
+        # scale the key scales of each row's window: every score there is
+        # 50x (the scores are linear in the key scale)
+        pos = torch.cat([torch.arange(n // 3, min(n, n // 3 + 3000)) for n in lens])
+        row = torch.cat([torch.full((min(n, n // 3 + 3000) - n // 3,), r) for r, n in enumerate(lens)])
+        ptc = pt.cpu()
+        pg = ptc[row, pos // 64].long().to(dev)
+        slot = (pos % 64).to(dev)
+        for ls in sets:
+            for L in ls:
+                if L.has_indexer:
+                    sc = L.index_k.view(num_pages, -1)[:, 8192:].view(torch.float32)
+                    sc[pg, slot] *= 50.0
     layers = sets[0]
     first = S.random_selection(lens, 2048, pt, seed=7, device=dev)
     torch.cuda.synchronize()
@@ -465,7 +482,7 @@ def main() -> int:
                    "topk": 2048, "page_tokens": 64,
                    "schedule": "MLI lag, one fused launch per layer, 1 hipGraph",
                    "hip_graph_packet_capture": packet_capture,
-                   "rotated_sets": n_sets, "bytes_per_step": step_bytes},
+                   "rotated_sets": n_sets, "bytes_per_step": step_bytes, "scores": args.scores},
         "tokens_per_s": round(B / (us_layer * 1e-6), 1),
         "indexer_scan_GBps": round(scan_gbs, 1),
         "layer_launch_us": round(launch_ms * 1e3, 3),

@@ -620,6 +620,168 @@ __device__ __forceinline__ uint32_t lane_rank(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
+// Workgroup i's share [part(n, i, nb), part(n, i + 1, nb)) of n items, in
+// 32-bit unsigned arithmetic (a 64-bit division is ~100 instructions, and
+// every instruction on this serial path costs ~2 ns): n * nb < 2^32, which
+// the launcher checks.
+__device__ __forceinline__ int part(int n, int i, int nb) {
+  return (int)(((uint32_t)n * (uint32_t)i) / (uint32_t)nb);
+}
+
+// Cooperative radix select, the published-list select's fallback when the
+// lists cannot decide (the row's top keys are packed into the positions of
+// a few workgroups, e.g. a recent-token window, or many equal scores).  The
+// row's workgroups still hold their own keys in LDS; together they find the
+// exact K-th key t* with three radix digits (key bits 31-20, 19-8, 7-0, the
+// digit structure of tilelang_dsa/topk_selector.py:36-194):
+//   each workgroup histograms the digit of its own keys that match the
+//   prefix so far, adds its non-zero bins to the row's global histogram of
+//   the pass (device-scope atomics), meets the others at a barrier, loads
+//   the summed histogram and takes the threshold bin (every workgroup reads
+//   the same sums, so all agree);
+// then every workgroup publishes its counts of finite keys above t* and of
+// keys equal to t*, and after one more barrier takes the counts of the
+// workgroups before it (its output offset).  Global areas of the row: the
+// pass-0 histogram in the standalone select's histogram (zero between
+// calls: cleared again here once read), passes 1 and 2 in its candidate
+// area (cleared here before use), the counts in its bitmap area (the
+// launcher keeps nb <= its words), the barrier counters in the otherwise
+// unused barrier areas 1 and 2: one set per launch parity (the list
+// barrier's sense), the other set is re-zeroed by every launch's list
+// barrier, so each launch starts from zero without a counter of its own.
+// Four barriers, no re-read of scores.
+struct RadixSel {
+  uint32_t tstar, need3, sel_before, ties_before, sel_above;
+};
+// A reusable barrier of the row's nb workgroups on monotonic counters (no
+// re-zeroing between uses): member bid arrives on group counter bid % 8; a
+// group's last arrival (its counter reaching use * group size) adds itself,
+// without waiting, to 8 replicated top counters, and each member polls the
+// replica of its XCD (bid % 8) until use * groups have arrived.  So no line
+// is both hit by many atomics and polled by many workgroups.  Lines (64
+// words each) of `ctr`: 0-7 group counters, 8-15 top replicas.  The wait is
+// bounded like the group barriers'.
+constexpr int kRadixGroups = 8;
+__host__ __device__ inline long radix_sync_off(int slab, uint32_t set) {
+  return row_sync_off(slab) + (1L + (long)set) * kSyncWords;
+}
+static_assert(2 * kRadixGroups <= kGroupSyncGroups + 1 + kGroupSyncFlags && kNumSync >= 4,
+              "the radix barrier's counter sets fit barrier areas 1 and 2");
+__device__ __forceinline__ void counter_barrier(uint32_t* ctr, int bid, int nb, uint32_t use) {
+  wait_mem();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int g = bid % kRadixGroups;
+    const uint32_t ng = (uint32_t)((nb - 1 - g) / kRadixGroups + 1);
+    const uint32_t ngroups = (uint32_t)min(nb, kRadixGroups);
+    if (__hip_atomic_fetch_add(&ctr[g * kGroupSyncLine], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+        use * ng - 1u)
+      for (int r = 0; r < kRadixGroups; ++r)
+        __hip_atomic_fetch_add(&ctr[(kRadixGroups + r) * kGroupSyncLine], 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t* top = &ctr[(kRadixGroups + bid % kRadixGroups) * kGroupSyncLine];
+    for (int i = 0; __hip_atomic_load(top, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < use * ngroups; ++i) {
+      if (i == kGroupSpinMax) {
+        atomicAdd(&g_group_wait_timeouts, 1);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  __syncthreads();
+}
+__device__ __forceinline__ RadixSel coop_radix(CoopShared& cs, uint32_t* rs, int slab, int bid, int nb, int nown,
+                                               uint32_t K, uint32_t set) {
+  const int t = threadIdx.x;
+  const int lane = t & (kWave - 1);
+  uint32_t* hist = cs.scan.hist;  // the union histogram is dead: 4096 words
+  uint32_t* g0 = rs + kHistOff;
+  uint32_t* g12 = rs + kBmOff + bitmap_words(slab);  // 2 x 4096 words
+  uint32_t* cnts = rs + kBmOff;
+  uint32_t* ctr = rs + radix_sync_off(slab, set);
+  uint32_t prefix = 0, need = K;
+#pragma unroll 1
+  for (int p = 0; p < 3; ++p) {
+    const int shift = p == 0 ? 20 : (p == 1 ? 8 : 0);
+    const int bits = p == 2 ? 8 : 12;
+    for (int i = t; i < kHistBins / 4; i += kMainThreads) reinterpret_cast<uint4*>(hist)[i] = make_uint4(0, 0, 0, 0);
+    __syncthreads();
+    for (int i = t; i < nown; i += kMainThreads) {
+      const uint32_t k = cs.keys[i];
+      if ((uint32_t)((uint64_t)k >> (shift + bits)) == prefix) atomicAdd(&hist[(k >> shift) & ((1u << bits) - 1u)], 1u);
+    }
+    __syncthreads();
+    dbg_stamp(blockIdx.x, 35 + 4 * p);
+    uint32_t* g = p == 0 ? g0 : g12 + (p - 1) * kHistBins;
+#pragma unroll
+    for (int j = 0; j < kHistBins / kMainThreads; ++j) {
+      const int i = t + j * kMainThreads;
+      const uint32_t v = hist[i];
+      if (v) __hip_atomic_fetch_add(&g[i], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (p == 0)  // passes 1 and 2 start from zero: cleared before anyone adds to them
+      for (int i = part(2 * kHistBins, bid, nb) + t; i < part(2 * kHistBins, bid + 1, nb); i += kMainThreads)
+        store_dev(&g12[i], 0u);
+    counter_barrier(ctr, bid, nb, (uint32_t)p + 1u);
+    dbg_stamp(blockIdx.x, 32 + 4 * p);
+    {
+      // thread t: bins 8t .. 8t + 7; eight threads sum a coarse bin of 64
+      static_assert(kHistBins == 8 * kMainThreads, "eight bins per thread");
+      const __amdgpu_buffer_rsrc_t r = dev_rsrc(g, 4u * kHistBins);
+      const uint4 a = load_dev16(r, 32u * (uint32_t)t), b = load_dev16(r, 32u * (uint32_t)t + 16u);
+      reinterpret_cast<uint4*>(hist)[2 * t] = a;
+      reinterpret_cast<uint4*>(hist)[2 * t + 1] = b;
+      uint32_t v = a.x + a.y + a.z + a.w + b.x + b.y + b.z + b.w;
+      v += __shfl_xor(v, 1);
+      v += __shfl_xor(v, 2);
+      v += __shfl_xor(v, 4);
+      if ((t & 7) == 0) hist[kCoarseOff + (t >> 3)] = v;
+    }
+    __syncthreads();
+    dbg_stamp(blockIdx.x, 33 + 4 * p);
+    // the row holds >= need keys with this prefix, so the bin exists
+    const BinThreshold th = wave_threshold(hist, need);
+    prefix = (prefix << bits) | th.bin;
+    need -= th.above;
+    dbg_stamp(blockIdx.x, 34 + 4 * p);
+    __syncthreads();  // hist is cleared next
+  }
+  RadixSel r{prefix, need, 0u, 0u, 0u};
+  uint32_t gt = 0, eq = 0;
+  for (int i = t; i < nown; i += kMainThreads) {
+    const uint32_t k = cs.keys[i];
+    gt += (k > prefix && key_is_finite(k)) ? 1u : 0u;
+    eq += k == prefix ? 1u : 0u;
+  }
+  const uint4 c = block_reduce4<0, 0, 0, 0>(make_uint4(gt, eq, 0u, 0u), cs.wave_tmp);
+  static_assert(kCoopKeys < 65536, "packed per-workgroup counts");
+  if (t == 0) store_dev(&cnts[bid], c.x | c.y << 16);
+  dbg_stamp(blockIdx.x, 44);
+  counter_barrier(ctr, bid, nb, 4u);
+  dbg_stamp(blockIdx.x, 45);
+  {
+    // every wave reduces all counts itself (lane l: workgroups l, l + 64, ...)
+    const __amdgpu_buffer_rsrc_t cr = dev_rsrc(cnts, 4u * (uint32_t)nb);
+    uint32_t sb = 0, tb = 0, sa = 0;
+#pragma unroll
+    for (int k = 0; k < kCoopMaxBlocks / kWave; ++k) {
+      const int j = lane + k * kWave;
+      const uint32_t w = load_dev4(cr, 4u * (uint32_t)j);  // 0 past nb
+      sb += j < bid ? (w & 0xffffu) : 0u;
+      tb += j < bid ? (w >> 16) : 0u;
+      sa += w & 0xffffu;
+    }
+    r.sel_before = wave_reduce<0>(sb);
+    r.ties_before = wave_reduce<0>(tb);
+    r.sel_above = wave_reduce<0>(sa);
+  }
+  dbg_stamp(blockIdx.x, 46);
+  // every workgroup has read the pass-0 histogram: clear this one's share
+  for (int i = part(kHistBins, bid, nb) + t; i < part(kHistBins, bid + 1, nb); i += kMainThreads) store_dev(&g0[i], 0u);
+  dbg_stamp(blockIdx.x, 47);
+  return r;
+}
+
 // Published-list form of the cooperative select (the default).  Each scan
 // workgroup of the row publishes every own key >= its bound lo_b (at most P
 // keys, the list's capacity; lo_b = 0 when it holds at most P), zero-padded,
@@ -632,10 +794,10 @@ __device__ __forceinline__ uint32_t lane_rank(uint64_t m) {
 // alone, finds the exact K-th key t* of their union and the ties to take.
 // The union holds every key >= t* of the row when it holds at least K keys
 // >= L = the largest bound (then t* >= L); the workgroups check that (they
-// all see the same lists, so they agree) and otherwise return false: the
-// caller then has the row selected by one workgroup over its scores in
-// memory (topk.hip finalize_row).  The offsets follow from the lists of the workgroups
-// before this one; each workgroup then writes its own selected positions
+// all see the same lists, so they agree) and otherwise run the cooperative
+// radix select over the keys they hold (coop_radix) for t* and the offsets.
+// From the lists, the offsets follow from the lists of the workgroups
+// before this one.  Each workgroup then writes its own selected positions
 // (KV slots) in position order.
 // Expects, from the scan: the own keys in cs.keys (position order), their
 // fine and coarse histograms, and cs.wstat.
@@ -645,7 +807,7 @@ __device__ __forceinline__ uint32_t lane_rank(uint64_t m) {
 // past the union they read as 0, below every bound, so every per-entry loop
 // runs NU times without a guard.
 template <bool TOPK, int NU>
-__device__ __forceinline__ bool coop_select(CoopShared& cs, unsigned char* smem, const ScanArgs& S, int bid,
+__device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem, const ScanArgs& S, int bid,
                                             int nb, int len, int p_lo, int p_hi, uint32_t* rs,
                                             const float* srow, const int* pt_row, int* o, const int* pts,
                                             int pg0, bool pts_lds) {
@@ -829,7 +991,8 @@ __device__ __forceinline__ bool coop_select(CoopShared& cs, unsigned char* smem,
     em_key = cs.keys[i];
     em_slot = slot_of(p_lo + i);
   }
-  group_wait_rep(sync, sync + 3 * kSyncWords, bid, nb, cs.sense[0]);
+  group_wait_rep(sync, sync + 3 * kSyncWords, bid, nb, cs.sense[0], rs + radix_sync_off(S.slab_stride, (cs.sense[0] & 1u) ^ 1u),
+                 2 * kRadixGroups);
   dbg_stamp(dbk, 9);
 
   // ---- every workgroup: all lists into registers (one batch of
@@ -880,6 +1043,7 @@ __device__ __forceinline__ bool coop_select(CoopShared& cs, unsigned char* smem,
   };
 
   uint32_t tstar = 0, need3 = 0;
+  bool radix = false;  // t* from the cooperative radix select: every own key is a candidate
   // sel_before = selected above t* before this workgroup, ties_before = ties
   // before it, sel_above = all selected above t*; all: finite counts
   uint32_t sel_before = 0, ties_before = 0, sel_above = 0;
@@ -919,7 +1083,18 @@ __device__ __forceinline__ bool coop_select(CoopShared& cs, unsigned char* smem,
       nbin = th.cnt;
     }
     dbg_stamp(dbk, 4);
-    if (!ok) return false;  // every workgroup decides alike (the same lists)
+    if (!ok) {
+      // the lists cannot decide (every workgroup sees the same lists, so
+      // all of them come here): the cooperative radix select over the keys
+      // the workgroups hold
+      const RadixSel rr = coop_radix(cs, rs, S.slab_stride, bid, nb, nown, (uint32_t)K, cs.sense[0] & 1u);
+      tstar = rr.tstar;
+      need3 = rr.need3;
+      sel_before = rr.sel_before;
+      ties_before = rr.ties_before;
+      sel_above = rr.sel_above;
+      radix = true;
+    } else {
     // pass 2: finite keys above T1's bin are selected: count them (and
     // those of the lists before this one; a list is a whole number of
     // uint4s); T1's bin -> candidates.  Edges: bin > T1 <=> w > top, and
@@ -1061,6 +1236,7 @@ __device__ __forceinline__ bool coop_select(CoopShared& cs, unsigned char* smem,
       ties_before = r.y;
       sel_above += r.z;
     }
+    }  // the lists decide
     dbg_stamp(dbk, 15);
   }
   const bool tfin = !all && key_is_finite(tstar);
@@ -1072,8 +1248,9 @@ __device__ __forceinline__ bool coop_select(CoopShared& cs, unsigned char* smem,
   // this workgroup's list (it is >= t* >= every list bound), which holds the
   // entries in position order: thread t takes contiguous entries.  A row of
   // <= K tokens publishes nothing and takes every finite key instead. ----
-  const int n_e = all ? nown : (int)cnt;
-  if (wave_emit) {
+  const bool walk_own = all || radix;  // the entries are all own keys, not the list
+  const int n_e = walk_own ? nown : (int)cnt;
+  if (wave_emit && !radix) {
     // a list of at most one wave's entries: wave 0 emits it, ranks by ballot
     if (wv == 0) {
       const bool in = lane < n_e;
@@ -1088,11 +1265,11 @@ __device__ __forceinline__ bool coop_select(CoopShared& cs, unsigned char* smem,
     if (bid == nb - 1)
       for (int j = (int)nsel + t; j < K; j += kMainThreads) o[j] = TOPK ? S.pad : -1;
     dbg_stamp(dbk, 11);
-    return true;
+    return;
   }
   const int per = (n_e + kMainThreads - 1) / kMainThreads;
   const int e0 = min(n_e, t * per), e1 = min(n_e, e0 + per);
-  const auto entry = [&](int e) { return all ? e : (int)lpos[e]; };  // -> own position index
+  const auto entry = [&](int e) { return walk_own ? e : (int)lpos[e]; };  // -> own position index
   uint32_t tie_rank = ties_before;  // rank among all ties of this thread's first tie
   bool any_tie = own_ties > 0;
   if (own_ties < 0) {
@@ -1134,7 +1311,6 @@ __device__ __forceinline__ bool coop_select(CoopShared& cs, unsigned char* smem,
   if (bid == nb - 1)
     for (int j = (int)nsel + t; j < K; j += kMainThreads) o[j] = TOPK ? S.pad : -1;
   dbg_stamp(dbk, 11);
-  return true;
 }
 
 template <int VARIANT>
@@ -1240,13 +1416,6 @@ __device__ __forceinline__ void select_row(unsigned char* smem, const float* sro
   for (int j = (int)run_sel + t; j < K; j += kT) o[j] = pad;
 }
 
-// Workgroup i's share [part(n, i, nb), part(n, i + 1, nb)) of n items, in
-// 32-bit unsigned arithmetic (a 64-bit division is ~100 instructions, and
-// every instruction on this serial path costs ~2 ns): n * nb < 2^32, which
-// the launcher checks.
-__device__ __forceinline__ int part(int n, int i, int nb) {
-  return (int)(((uint32_t)n * (uint32_t)i) / (uint32_t)nb);
-}
 
 // FROM_SCORES: the row's scores are already in the slab (a plain scan
 // launch wrote them); the workgroup loads its positions' scores instead of
@@ -1525,22 +1694,27 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
     int* o = S.next_idx + (long)row * S.topk;
     const int p_hi = min(c1 * kChunkKeys, len);
     const bool narrow = nb * pub_stride(nb, S.topk) <= 4 * 4 * kMainThreads;
-    bool decided;
-    if constexpr (LISTS == 4)
-      decided = narrow && coop_select<TOPK, 4>(cs, smem, S, bid, nb, len, c0 * kChunkKeys, p_hi, rs, srow, pt_row,
-                                               o, sh.pts, pg0, pts_lds);
-    else if constexpr (LISTS == 8)
-      decided = coop_select<TOPK, 8>(cs, smem, S, bid, nb, len, c0 * kChunkKeys, p_hi, rs, srow, pt_row, o,
-                                     sh.pts, pg0, pts_lds);
-    else
-      decided = narrow ? coop_select<TOPK, 4>(cs, smem, S, bid, nb, len, c0 * kChunkKeys, p_hi, rs, srow, pt_row,
-                                              o, sh.pts, pg0, pts_lds)
-                       : coop_select<TOPK, 8>(cs, smem, S, bid, nb, len, c0 * kChunkKeys, p_hi, rs, srow, pt_row,
-                                              o, sh.pts, pg0, pts_lds);
-    if (decided) return;
-    // the lists could not decide (e.g. many equal scores): the row is
-    // selected by one workgroup over its scores in memory, as without the
-    // cooperative select
+    if constexpr (LISTS == 4) {
+      if (narrow) {
+        coop_select<TOPK, 4>(cs, smem, S, bid, nb, len, c0 * kChunkKeys, p_hi, rs, srow, pt_row, o, sh.pts, pg0,
+                             pts_lds);
+        return;
+      }
+      // (not sent by the launcher) too many list entries for this form: the
+      // single-workgroup select below
+    } else if constexpr (LISTS == 8) {
+      coop_select<TOPK, 8>(cs, smem, S, bid, nb, len, c0 * kChunkKeys, p_hi, rs, srow, pt_row, o, sh.pts, pg0,
+                           pts_lds);
+      return;
+    } else {
+      if (narrow)
+        coop_select<TOPK, 4>(cs, smem, S, bid, nb, len, c0 * kChunkKeys, p_hi, rs, srow, pt_row, o, sh.pts, pg0,
+                             pts_lds);
+      else
+        coop_select<TOPK, 8>(cs, smem, S, bid, nb, len, c0 * kChunkKeys, p_hi, rs, srow, pt_row, o, sh.pts, pg0,
+                             pts_lds);
+      return;
+    }
   }
   // arrival: wait for this slice's device-scope score stores, then count;
   // the row's last slice selects

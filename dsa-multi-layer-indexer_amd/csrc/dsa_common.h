@@ -151,7 +151,7 @@ __device__ __forceinline__ float wave_max(float v) {
 // `ph`; the internal dsa_internal_debug entry point clears the table.
 // Counterpart of the reference's hp_dbg stamps (K:1076-1091).
 constexpr int kDbgBlocks = 512;
-constexpr int kDbgPhases = 32;
+constexpr int kDbgPhases = 48;
 extern __device__ int g_dbg_on;
 extern __device__ unsigned long long g_dbg[kDbgBlocks * kDbgPhases];
 #ifdef DSA_PHASE_STAMPS
@@ -288,7 +288,10 @@ __device__ __forceinline__ void group_arrive_rep(uint32_t* sync, uint32_t* tops,
   }
 }
 // Wait half: returns (to every thread) once all nb members have arrived.
-__device__ __forceinline__ void group_wait_rep(uint32_t* sync, uint32_t* tops, int bid, int nb, uint32_t sense) {
+// Workgroup 0 also zeroes `nclr` lines of `clr` (another structure's next
+// counter set) with the next set's counters.
+__device__ __forceinline__ void group_wait_rep(uint32_t* sync, uint32_t* tops, int bid, int nb, uint32_t sense,
+                                               uint32_t* clr = nullptr, int nclr = 0) {
   const uint32_t set = sense & 1u;
   if (threadIdx.x == 0) {
     const uint32_t ngroups = (uint32_t)min(nb, kRepGroups);
@@ -309,6 +312,8 @@ __device__ __forceinline__ void group_wait_rep(uint32_t* sync, uint32_t* tops, i
       store_dev(&tops[((set ^ 1u) * kRepTops + (t - kRepGroups)) * kGroupSyncLine], 0u);
     else if (t < kRepGroups + kRepTops + kGroupSyncFlags)
       store_dev(&sync[(kGroupSyncGroups + 1 + (t - kRepGroups - kRepTops)) * kGroupSyncLine], sense ^ 1u);
+    else if (t < kRepGroups + kRepTops + kGroupSyncFlags + nclr)
+      store_dev(&clr[(t - kRepGroups - kRepTops - kGroupSyncFlags) * kGroupSyncLine], 0u);
   }
 }
 
