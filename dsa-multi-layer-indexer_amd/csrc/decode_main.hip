@@ -652,6 +652,7 @@ __device__ __forceinline__ int part(int n, int i, int nb) {
 // Four barriers, no re-read of scores.
 struct RadixSel {
   uint32_t tstar, need3, sel_before, ties_before, sel_above;
+  uint32_t own_gt, own_eq;  // this workgroup's finite keys above t*, keys equal to t*
 };
 // A reusable barrier of the row's nb workgroups on monotonic counters (no
 // re-zeroing between uses): member bid arrives on group counter bid % 8; a
@@ -699,7 +700,29 @@ __device__ __forceinline__ RadixSel coop_radix(CoopShared& cs, uint32_t* rs, int
   uint32_t* g12 = rs + kBmOff + bitmap_words(slab);  // 2 x 4096 words
   uint32_t* cnts = rs + kBmOff;
   uint32_t* ctr = rs + radix_sync_off(slab, set);
+  // A lower bound on t* from the list headers: workgroup b holds count_b
+  // keys >= its list bound lo_b, so if the workgroups whose bound lies in
+  // 12-bit bins >= TB hold >= K such keys together, t* >= TB's lower edge,
+  // and pass 0 need only count keys in bins >= TB (exact counts there are
+  // all the threshold search reads).  This spares most workgroups most of
+  // their pass-0 atomics, which contend on the same bins of the row.
+  uint32_t tb = 0;
+  {
+    for (int i = t; i < kHistWords / 4; i += kMainThreads) reinterpret_cast<uint4*>(hist)[i] = make_uint4(0, 0, 0, 0);
+    __syncthreads();
+    if (t < nb) {
+      const uint4 h = load_dev16(dev_rsrc(rs + row_pub_off(slab), 16u * (uint32_t)nb), 16u * (uint32_t)t);
+      if (h.x > 0u && h.y != kNoKeys) {  // count, bound
+        atomicAdd(&hist[h.y >> 20], h.x);
+        atomicAdd(&hist[kCoarseOff + (h.y >> 26)], h.x);
+      }
+    }
+    __syncthreads();
+    const BinThreshold th = wave_threshold(hist, K);
+    tb = th.total >= K ? th.bin : 0u;
+  }
   uint32_t prefix = 0, need = K;
+  uint32_t uses = 0;  // barriers passed (the counters' targets grow by one use each)
 #pragma unroll 1
   for (int p = 0; p < 3; ++p) {
     const int shift = p == 0 ? 20 : (p == 1 ? 8 : 0);
@@ -708,7 +731,8 @@ __device__ __forceinline__ RadixSel coop_radix(CoopShared& cs, uint32_t* rs, int
     __syncthreads();
     for (int i = t; i < nown; i += kMainThreads) {
       const uint32_t k = cs.keys[i];
-      if ((uint32_t)((uint64_t)k >> (shift + bits)) == prefix) atomicAdd(&hist[(k >> shift) & ((1u << bits) - 1u)], 1u);
+      if (p == 0 ? (k >> 20) >= tb : (k >> (p == 1 ? 20 : 8)) == prefix)
+        atomicAdd(&hist[(k >> shift) & ((1u << bits) - 1u)], 1u);
     }
     __syncthreads();
     dbg_stamp(blockIdx.x, 35 + 4 * p);
@@ -722,7 +746,7 @@ __device__ __forceinline__ RadixSel coop_radix(CoopShared& cs, uint32_t* rs, int
     if (p == 0)  // passes 1 and 2 start from zero: cleared before anyone adds to them
       for (int i = part(2 * kHistBins, bid, nb) + t; i < part(2 * kHistBins, bid + 1, nb); i += kMainThreads)
         store_dev(&g12[i], 0u);
-    counter_barrier(ctr, bid, nb, (uint32_t)p + 1u);
+    counter_barrier(ctr, bid, nb, ++uses);
     dbg_stamp(blockIdx.x, 32 + 4 * p);
     {
       // thread t: bins 8t .. 8t + 7; eight threads sum a coarse bin of 64
@@ -745,19 +769,31 @@ __device__ __forceinline__ RadixSel coop_radix(CoopShared& cs, uint32_t* rs, int
     need -= th.above;
     dbg_stamp(blockIdx.x, 34 + 4 * p);
     __syncthreads();  // hist is cleared next
+    // the whole bin is taken: every key >= its lower edge is selected, the
+    // rest is not, so t* = edge - 1 with no ties to take (every workgroup
+    // sees the same sums and stops alike).  The edge is > 0: the lowest bin
+    // of a pass cannot hold the row's last K keys of more than K.
+    const uint32_t edge = prefix << shift;
+    if (th.cnt == need && edge > 0u) {
+      prefix = edge - 1u;
+      need = 0u;
+      break;
+    }
   }
-  RadixSel r{prefix, need, 0u, 0u, 0u};
+  RadixSel r{prefix, need, 0u, 0u, 0u, 0u, 0u};
   uint32_t gt = 0, eq = 0;
   for (int i = t; i < nown; i += kMainThreads) {
     const uint32_t k = cs.keys[i];
     gt += (k > prefix && key_is_finite(k)) ? 1u : 0u;
-    eq += k == prefix ? 1u : 0u;
+    eq += (need && k == prefix) ? 1u : 0u;
   }
   const uint4 c = block_reduce4<0, 0, 0, 0>(make_uint4(gt, eq, 0u, 0u), cs.wave_tmp);
+  r.own_gt = c.x;
+  r.own_eq = c.y;
   static_assert(kCoopKeys < 65536, "packed per-workgroup counts");
   if (t == 0) store_dev(&cnts[bid], c.x | c.y << 16);
   dbg_stamp(blockIdx.x, 44);
-  counter_barrier(ctr, bid, nb, 4u);
+  counter_barrier(ctr, bid, nb, ++uses);
   dbg_stamp(blockIdx.x, 45);
   {
     // every wave reduces all counts itself (lane l: workgroups l, l + 64, ...)
@@ -1044,6 +1080,7 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
 
   uint32_t tstar = 0, need3 = 0;
   bool radix = false;  // t* from the cooperative radix select: every own key is a candidate
+  uint32_t radix_own = 0;  // then: this workgroup's selected keys
   // sel_before = selected above t* before this workgroup, ties_before = ties
   // before it, sel_above = all selected above t*; all: finite counts
   uint32_t sel_before = 0, ties_before = 0, sel_above = 0;
@@ -1093,6 +1130,8 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
       sel_before = rr.sel_before;
       ties_before = rr.ties_before;
       sel_above = rr.sel_above;
+      own_ties = (int)rr.own_eq;
+      radix_own = rr.own_gt + (key_is_finite(tstar) ? min(rr.own_eq, need3 - min(ties_before, need3)) : 0u);
       radix = true;
     } else {
     // pass 2: finite keys above T1's bin are selected: count them (and
@@ -1265,6 +1304,11 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
     if (bid == nb - 1)
       for (int j = (int)nsel + t; j < K; j += kMainThreads) o[j] = TOPK ? S.pad : -1;
     dbg_stamp(dbk, 11);
+    return;
+  }
+  if (radix && radix_own == 0u) {  // nothing of this workgroup's is selected
+    if (bid == nb - 1)
+      for (int j = (int)nsel + t; j < K; j += kMainThreads) o[j] = TOPK ? S.pad : -1;
     return;
   }
   const int per = (n_e + kMainThreads - 1) / kMainThreads;

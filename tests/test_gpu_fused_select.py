@@ -41,12 +41,21 @@ def _layer(dev, lens, seed, pattern=None):
     elif pattern == "equal":  # every key and scale identical: all scores equal
         pages[:, :8192] = pages[0, :128].repeat(64)
         pages[:, 8192:].view(torch.float32).fill_(1.0)
-    elif pattern == "window":  # a 3000-token window of each row scores far above the rest
+    elif pattern is not None and pattern.startswith("window"):
+        # a window of each row scores far above the rest: "window" 3000
+        # tokens from len/3; "window_end" the last 4096 tokens (recent
+        # tokens); "window_small" 1000 tokens (the rest of the top-K spread
+        # over the row); "window_dup" the window over repeated pages (many
+        # equal scores at the threshold)
+        if pattern == "window_dup":
+            src = pages[:8].clone()
+            for p in range(num_pages):
+                pages[p] = src[p % 8]
         scales = pages[:, 8192:].view(torch.float32)  # [page][token in page]
         ptc = pt.cpu().numpy()
         for r, n in enumerate(lens):
-            a = n // 3
-            for pos in range(a, min(n, a + 3000)):
+            a, w = {"window_end": (max(0, n - 4096), 4096), "window_small": (n // 2, 1000)}.get(pattern, (n // 3, 3000))
+            for pos in range(a, min(n, a + w)):
                 scales[int(ptc[r, pos // 64]), pos % 64] *= 50.0
     return L, pt
 
@@ -86,6 +95,11 @@ CASES = [
     ([131072], 13, "window"),
     ([131072, 70000, 9000], 14, "window"),
     ([20000] * 9, 15, "window"),
+    ([131072], 16, "window_end"),
+    ([131072, 65536], 17, "window_small"),
+    ([131072], 18, "window_dup"),
+    ([100000, 3000, 50000], 19, "window_end"),
+    ([30000] * 10, 20, "window_small"),
 ]
 
 
