@@ -353,9 +353,23 @@ extern "C" {
 
 const char* dsa_last_error(void) { return g_err; }
 
-const char* dsa_version(void) { return "dsa_mli 0.3.0 gfx950"; }
+const char* dsa_version(void) { return "dsa_mli 0.4.0 gfx950"; }
 
 int dsa_sync_timeouts(int reset) { return dsa::group_wait_timeouts(reset); }
+
+int dsa_sync_status(const void* topk_scratch, int B_scan, int slab_stride, const void* workspace, int B_attn,
+                    int H, int32_t* status, int clear, void* stream) {
+  DSA_REQUIRE(status, DSA_ERR_INVALID_ARG, "dsa_sync_status: null status pointer");
+  DSA_REQUIRE(!topk_scratch || (B_scan >= 1 && slab_stride >= 1 && slab_stride <= DSA_TOPK_MAX_CTX),
+              DSA_ERR_INVALID_ARG, "dsa_sync_status: bad top-k scratch shape (B_scan %d, slab_stride %d)", B_scan,
+              slab_stride);
+  DSA_REQUIRE(!workspace || (B_attn >= 1 && H >= 16 && H % 16 == 0), DSA_ERR_INVALID_ARG,
+              "dsa_sync_status: bad workspace shape (B_attn %d, H %d)", B_attn, H);
+  return hip_status(dsa::launch_sync_status(const_cast<void*>(topk_scratch), B_scan, slab_stride,
+                                            const_cast<void*>(workspace), workspace ? B_attn * (H / 16) : 0,
+                                            status, clear ? 1 : 0, (hipStream_t)stream),
+                    "sync status launch");
+}
 
 int dsa_indexer_scan(const void* q_fp8, const float* w, const void* index_k, int64_t num_pages,
                      const int32_t* page_table, const int32_t* seq_lens, float* scores, int B,
@@ -594,6 +608,14 @@ extern "C" int dsa_internal_set_coop_select(int on) {
   return DSA_OK;
 }
 extern "C" int dsa_internal_group_wait_timeouts(int reset) { return dsa::group_wait_timeouts(reset); }
+// Internal test hook: polls before an in-launch wait gives up (n < 0: the
+// default, about a second).  n = 0 makes every wait that is not already
+// satisfied give up at once, so tests can check expiry reporting without a
+// kernel that waits for long.
+extern "C" int dsa_internal_set_spin_limit(int n) {
+  dsa::set_spin_limit(n);
+  return DSA_OK;
+}
 extern "C" int dsa_internal_set_scan_blocks_cap(int n) {
   dsa::set_scan_blocks_cap(n);
   return DSA_OK;

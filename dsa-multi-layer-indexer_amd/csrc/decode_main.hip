@@ -668,7 +668,7 @@ __host__ __device__ inline long radix_sync_off(int slab, uint32_t set) {
 }
 static_assert(2 * kRadixGroups <= kGroupSyncGroups + 1 + kGroupSyncFlags && kNumSync >= 4,
               "the radix barrier's counter sets fit barrier areas 1 and 2");
-__device__ __forceinline__ void counter_barrier(uint32_t* ctr, int bid, int nb, uint32_t use) {
+__device__ __forceinline__ void counter_barrier(uint32_t* ctr, int bid, int nb, uint32_t use, uint32_t* status) {
   wait_mem();
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -681,9 +681,10 @@ __device__ __forceinline__ void counter_barrier(uint32_t* ctr, int bid, int nb, 
         __hip_atomic_fetch_add(&ctr[(kRadixGroups + r) * kGroupSyncLine], 1u, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
     const uint32_t* top = &ctr[(kRadixGroups + bid % kRadixGroups) * kGroupSyncLine];
+    const int lim = g_group_spin_max;
     for (int i = 0; __hip_atomic_load(top, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < use * ngroups; ++i) {
-      if (i == kGroupSpinMax) {
-        atomicAdd(&g_group_wait_timeouts, 1);
+      if (i == lim) {
+        wait_expired(status);
         break;
       }
       __builtin_amdgcn_s_sleep(1);
@@ -700,6 +701,7 @@ __device__ __forceinline__ RadixSel coop_radix(CoopShared& cs, uint32_t* rs, int
   uint32_t* g12 = rs + kBmOff + bitmap_words(slab);  // 2 x 4096 words
   uint32_t* cnts = rs + kBmOff;
   uint32_t* ctr = rs + radix_sync_off(slab, set);
+  uint32_t* status = rs + row_sync_off(slab) + kSyncStatusWord;  // the row's, as for the list barrier
   // A lower bound on t* from the list headers: workgroup b holds count_b
   // keys >= its list bound lo_b, so if the workgroups whose bound lies in
   // 12-bit bins >= TB hold >= K such keys together, t* >= TB's lower edge,
@@ -746,7 +748,7 @@ __device__ __forceinline__ RadixSel coop_radix(CoopShared& cs, uint32_t* rs, int
     if (p == 0)  // passes 1 and 2 start from zero: cleared before anyone adds to them
       for (int i = part(2 * kHistBins, bid, nb) + t; i < part(2 * kHistBins, bid + 1, nb); i += kMainThreads)
         store_dev(&g12[i], 0u);
-    counter_barrier(ctr, bid, nb, ++uses);
+    counter_barrier(ctr, bid, nb, ++uses, status);
     dbg_stamp(blockIdx.x, 32 + 4 * p);
     {
       // thread t: bins 8t .. 8t + 7; eight threads sum a coarse bin of 64
@@ -793,7 +795,7 @@ __device__ __forceinline__ RadixSel coop_radix(CoopShared& cs, uint32_t* rs, int
   static_assert(kCoopKeys < 65536, "packed per-workgroup counts");
   if (t == 0) store_dev(&cnts[bid], c.x | c.y << 16);
   dbg_stamp(blockIdx.x, 44);
-  counter_barrier(ctr, bid, nb, ++uses);
+  counter_barrier(ctr, bid, nb, ++uses, status);
   dbg_stamp(blockIdx.x, 45);
   {
     // every wave reduces all counts itself (lane l: workgroups l, l + 64, ...)
@@ -1879,6 +1881,49 @@ int group_wait_timeouts(int reset) {
     if (hipMemcpyToSymbol(HIP_SYMBOL(g_group_wait_timeouts), &z, sizeof(int)) != hipSuccess) return -1;
   }
   return v;
+}
+
+void set_spin_limit(int n) {
+  const int v = n < 0 ? kGroupSpinMax : n;
+  (void)hipMemcpyToSymbol(HIP_SYMBOL(g_group_spin_max), &v, sizeof(int));
+}
+
+// Sum of the status words (expired waits) of nrows top-k scratch rows and
+// ngroups attention barrier areas into *out, optionally re-zeroed.  One
+// workgroup; the words are read with device-scope loads.
+constexpr int kStatusThreads = 256;
+__global__ __launch_bounds__(kStatusThreads) void sync_status_kernel(uint32_t* scr, int nrows, long row_words,
+                                                                     long row_off, uint32_t* ws, int ngroups,
+                                                                     int* out, int clear) {
+  __shared__ uint32_t part[kStatusThreads / kWave];
+  const int t = threadIdx.x;
+  uint32_t v = 0;
+  for (int i = t; i < nrows; i += kStatusThreads) {
+    uint32_t* p = scr + (long)i * row_words + row_off;
+    v += __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (clear) store_dev(p, 0u);
+  }
+  for (int i = t; i < ngroups; i += kStatusThreads) {
+    uint32_t* p = ws + (long)i * kSyncWords + kSyncStatusWord;
+    v += __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (clear) store_dev(p, 0u);
+  }
+  v = wave_reduce<0>(v);
+  if ((t & (kWave - 1)) == 0) part[t / kWave] = v;
+  __syncthreads();
+  if (t == 0) {
+    uint32_t tot = 0;
+    for (int w = 0; w < kStatusThreads / kWave; ++w) tot += part[w];
+    out[0] = (int)min(tot, 0x7fffffffu);
+  }
+}
+
+hipError_t launch_sync_status(void* topk_scratch, int B_scan, int slab, void* workspace, int groups, int* out,
+                              int clear, hipStream_t s) {
+  hipLaunchKernelGGL(sync_status_kernel, dim3(1), dim3(kStatusThreads), 0, s, static_cast<uint32_t*>(topk_scratch),
+                     topk_scratch ? B_scan : 0, row_scratch_words(slab), row_sync_off(slab) + kSyncStatusWord,
+                     static_cast<uint32_t*>(workspace), workspace ? groups : 0, out, clear);
+  return hipGetLastError();
 }
 
 static int device_cus() {

@@ -248,6 +248,18 @@ __device__ __forceinline__ uint32_t load_dev4(__amdgpu_buffer_rsrc_t r, uint32_t
 // counter says so) instead of hanging the device.
 extern __device__ int g_group_wait_timeouts;
 constexpr int kGroupSpinMax = 1 << 20;
+// polls before a wait gives up (kGroupSpinMax; lowered only by the library's
+// internal test hook, so that tests can make every wait give up at once)
+extern __device__ int g_group_spin_max;
+// The status word of a group: word 1 of line 0 of its barrier area (no
+// barrier uses it).  Each wait of the group's members that expires adds 1
+// there as well as to the process-wide count, so the caller can tell which
+// buffers (which launch's rows and head groups) were affected.
+constexpr int kSyncStatusWord = 1;
+__device__ __forceinline__ void wait_expired(uint32_t* status) {
+  atomicAdd(&g_group_wait_timeouts, 1);
+  atomicAdd(status, 1u);
+}
 constexpr int kGroupSyncGroups = 16, kGroupSyncFlags = 8, kGroupSyncLine = 64;
 constexpr int kGroupFlatMax = 32;  // groups up to this size use one arrival counter
 __device__ __forceinline__ uint32_t group_sense(const uint32_t* sync, int bid) {
@@ -296,9 +308,10 @@ __device__ __forceinline__ void group_wait_rep(uint32_t* sync, uint32_t* tops, i
   if (threadIdx.x == 0) {
     const uint32_t ngroups = (uint32_t)min(nb, kRepGroups);
     const uint32_t* top = &tops[(set * kRepTops + bid % kRepTops) * kGroupSyncLine];
+    const int lim = g_group_spin_max;
     for (int i = 0; __hip_atomic_load(top, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < ngroups; ++i) {
-      if (i == kGroupSpinMax) {
-        atomicAdd(&g_group_wait_timeouts, 1);
+      if (i == lim) {
+        wait_expired(&sync[kSyncStatusWord]);
         break;
       }
       __builtin_amdgcn_s_sleep(1);
@@ -339,9 +352,10 @@ __device__ __forceinline__ void group_barrier(uint32_t* sync, int bid, int nb, u
       for (int f = 0; f < kGroupSyncFlags; ++f)
         store_dev(&sync[(kGroupSyncGroups + 1 + f) * kGroupSyncLine], sense ^ 1u);
     } else {
+      const int lim = g_group_spin_max;
       for (int i = 0; group_sense(sync, bid) == sense; ++i) {
-        if (i == kGroupSpinMax) {
-          atomicAdd(&g_group_wait_timeouts, 1);
+        if (i == lim) {
+          wait_expired(&sync[kSyncStatusWord]);
           break;
         }
         __builtin_amdgcn_s_sleep(1);

@@ -65,6 +65,11 @@ void set_scan_variant(int v);
 void set_coop_select(int on);
 void set_scan_blocks_cap(int n);
 int group_wait_timeouts(int reset);
+void set_spin_limit(int n);  // < 0: the default
+// Sum of the expired-wait status words of B_scan top-k scratch rows and
+// `groups` attention barrier areas (B * H/16) into *out (device int).
+hipError_t launch_sync_status(void* topk_scratch, int B_scan, int slab, void* workspace, int groups, int* out,
+                              int clear, hipStream_t s);
 int attn_auto_nsplit(int topk, int B, int H);
 int attn_fused_nsplit(int topk, int B, int H);
 size_t attn_workspace_bytes(int B, int H, int nsplit);

@@ -37,6 +37,7 @@ namespace dsa {
 __device__ int g_dbg_on = 0;
 __device__ unsigned long long g_dbg[kDbgBlocks * kDbgPhases];
 __device__ int g_group_wait_timeouts = 0;
+__device__ int g_group_spin_max = kGroupSpinMax;
 
 constexpr int kNB1 = 4096;      // first digit: key bits [31:20]
 constexpr int kNB2 = 1024;      // refinements: bits [19:10], [9:0]

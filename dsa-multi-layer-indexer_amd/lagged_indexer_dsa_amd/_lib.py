@@ -69,6 +69,7 @@ SIGNATURES = {
     "dsa_last_error": (ctypes.c_char_p, []),
     "dsa_version": (ctypes.c_char_p, []),
     "dsa_sync_timeouts": (_i32, [_i32]),
+    "dsa_sync_status": (_i32, [_vp, _i32, _i32, _vp, _i32, _i32, _vp, _i32, _vp]),
     "dsa_indexer_scan": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp]),
     "dsa_topk_scratch_bytes": (ctypes.c_size_t, [_i32, _i32]),
     "dsa_topk": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
@@ -110,6 +111,8 @@ def load(path: Path | None = None) -> ctypes.CDLL:
     lib.dsa_internal_set_coop_select.argtypes = [_i32]
     lib.dsa_internal_group_wait_timeouts.restype = _i32
     lib.dsa_internal_group_wait_timeouts.argtypes = [_i32]
+    lib.dsa_internal_set_spin_limit.restype = _i32
+    lib.dsa_internal_set_spin_limit.argtypes = [_i32]
     _LIB = lib
     return lib
 

@@ -90,6 +90,26 @@ class DecodeLayer:
         a.dense = 1 if (self.dense and attention) else 0
         return a
 
+    def sync_status(self, clear: bool = True) -> int:
+        """Expired in-launch waits recorded in this layer's buffers (its
+        rows' selects and its attention's split merges) since the last
+        clear (dsa_sync_status); synchronises.  Nonzero means a launch of
+        this layer broke the co-residency assumption and its results are
+        wrong."""
+        if not hasattr(self, "_status"):
+            self._status = torch.zeros(1, dtype=torch.int32, device=self.q_bf16.device)
+        B, H, _ = self.q_bf16.shape
+        _lib.call("dsa_sync_status", self.topk_scratch.data_ptr(), B, self.slab_stride,
+                  self.workspace.data_ptr(), B, H, self._status.data_ptr(), 1 if clear else 0,
+                  torch.cuda.current_stream().cuda_stream)
+        return int(self._status.item())
+
+    def check_sync(self) -> None:
+        """Raise if any in-launch wait of this layer's launches expired."""
+        n = self.sync_status(clear=True)
+        if n:
+            raise _lib.DsaError(_lib.DSA_ERR_HIP, f"{n} in-launch waits expired: this layer's results are invalid")
+
     def run(self, attend_idx: torch.Tensor | None = None) -> None:
         """One layer on the current stream: indexer -> next_idx, attention
         over attend_idx (lagged) or over next_idx (same-layer, baseline DSA),
@@ -156,6 +176,11 @@ class MLISchedule:
         if self._graph is None:
             self.capture()
         _lib.call("dsa_mli_graph_launch", self._graph, torch.cuda.current_stream().cuda_stream)
+
+    def sync_status(self, clear: bool = True) -> int:
+        """Expired in-launch waits over every layer's buffers (see
+        DecodeLayer.sync_status); synchronises."""
+        return sum(layer.sync_status(clear) for layer in self.layers)
 
     def close(self) -> None:
         if self._graph is not None:

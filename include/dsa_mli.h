@@ -82,6 +82,24 @@ const char* dsa_version(void);
 int dsa_sync_timeouts(int reset);
 
 /*
+ * The same expiries per buffer, asynchronously: every wait that expires also
+ * adds 1 to a status word of its group in the caller's buffers -- one per
+ * top-k scratch row (the row's select) and one per (row, 16-head group) of
+ * a sparse-MLA workspace (the split merge).  This enqueues ONE small kernel
+ * on `stream` that writes into *status (a device int32) the sum of the
+ * words of the first B_scan rows of topk_scratch (slab_stride as it was
+ * allocated with) and of the B_attn*(H/16) groups of workspace, and zeroes
+ * them when clear != 0.  Either buffer may be NULL.  It never synchronises
+ * and may be captured in a graph (after the launches it covers), so a
+ * caller can check each step's launches when it next reads *status: 0 means
+ * every in-launch wait of those buffers was satisfied.
+ * No counterpart in the reference (its waits are unbounded).
+ */
+int dsa_sync_status(const void* topk_scratch, int B_scan, int slab_stride,
+                    const void* workspace, int B_attn, int H, int32_t* status,
+                    int clear, void* stream);
+
+/*
  * (1) Lightning-indexer scan.
  *   scores[b, g] = kscale[g] * sum_h w[b,h] * ReLU( sum_d q[b,h,d] * k[g,d] )
  * for g < seq_lens[b]; scores[b, g] = -inf for seq_lens[b] <= g < slab_stride.

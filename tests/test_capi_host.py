@@ -151,3 +151,14 @@ def test_operand_prep_contract(lib):
     assert lib.dsa_append_latent_rows(16, None, 2, 16, 8, None) == DSA_ERR_INVALID_ARG
     assert lib.dsa_append_latent_rows(16, 16, 2, 16, 0, None) == DSA_ERR_INVALID_ARG
     assert lib.dsa_append_latent_rows(None, None, 0, None, 0, None) == DSA_OK
+
+
+def test_sync_status_contract(lib):
+    from lagged_indexer_dsa_amd._lib import DSA_ERR_INVALID_ARG
+
+    f = lib.dsa_sync_status
+    assert f(16, 1, 1000, 16, 1, 16, None, 1, None) == DSA_ERR_INVALID_ARG   # no status word
+    assert f(16, 0, 1000, None, 0, 0, 16, 1, None) == DSA_ERR_INVALID_ARG    # B_scan < 1
+    assert f(16, 1, 300000, None, 0, 0, 16, 1, None) == DSA_ERR_INVALID_ARG  # slab too long
+    assert f(None, 0, 0, 16, 1, 24, 16, 1, None) == DSA_ERR_INVALID_ARG      # H not a multiple of 16
+    assert b"dsa_sync_status" in lib.dsa_last_error()
