@@ -115,6 +115,8 @@ int check_layer(const dsa_layer_args* a, bool in_schedule = false) {
   if (a->q_bf16 && a->dense) {
     DSA_REQUIRE(a->page_table && a->seq_lens && a->pt_stride >= 1, DSA_ERR_INVALID_ARG,
                 "dsa_decode_layer: dense attention needs page_table, pt_stride and seq_lens");
+    DSA_REQUIRE((int64_t)a->pt_stride * DSA_PAGE_TOKENS <= (int64_t)1 << 30, DSA_ERR_UNSUPPORTED,
+                "dsa_decode_layer: dense attention over pt_stride*64 keys must be <= 2^30");
     rc = check_mla(a->q_bf16, a->kv_pool, a->kv_rows, nullptr, a->workspace, a->out_bf16, a->B, a->H,
                    a->pt_stride * DSA_PAGE_TOKENS, a->nsplit, /*idx_required=*/false);
     if (rc) return rc;
@@ -354,6 +356,8 @@ extern "C" {
 const char* dsa_last_error(void) { return g_err; }
 
 const char* dsa_version(void) { return "dsa_mli 0.4.0 gfx950"; }
+
+size_t dsa_layer_args_bytes(void) { return sizeof(dsa_layer_args); }
 
 int dsa_sync_timeouts(int reset) { return dsa::group_wait_timeouts(reset); }
 

@@ -68,6 +68,7 @@ _LIB: ctypes.CDLL | None = None
 SIGNATURES = {
     "dsa_last_error": (ctypes.c_char_p, []),
     "dsa_version": (ctypes.c_char_p, []),
+    "dsa_layer_args_bytes": (ctypes.c_size_t, []),
     "dsa_sync_timeouts": (_i32, [_i32]),
     "dsa_sync_status": (_i32, [_vp, _i32, _i32, _vp, _i32, _i32, _vp, _i32, _vp]),
     "dsa_indexer_scan": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp]),
@@ -105,6 +106,9 @@ def load(path: Path | None = None) -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
+    if lib.dsa_layer_args_bytes() != ctypes.sizeof(LayerArgs):
+        raise RuntimeError(f"{p}: dsa_layer_args is {lib.dsa_layer_args_bytes()} bytes in the library, "
+                           f"{ctypes.sizeof(LayerArgs)} in this binding (header mismatch)")
     lib.dsa_internal_set_scan_variant.restype = _i32
     lib.dsa_internal_set_scan_variant.argtypes = [_i32]
     lib.dsa_internal_set_coop_select.restype = _i32

@@ -61,6 +61,10 @@ const char* dsa_last_error(void);
 /* Library version string. */
 const char* dsa_version(void);
 
+/* sizeof(dsa_layer_args) as the library was built: a caller compares it with
+ * its own sizeof to detect a header mismatch (0.3 appended `dense`). */
+size_t dsa_layer_args_bytes(void);
+
 /*
  * Count of in-launch group waits that expired on the current device since
  * the library was loaded (or since the last call with reset != 0); reset != 0
@@ -209,8 +213,7 @@ int dsa_dense_mla_decode(const void* q_bf16, const void* kv_pool, int64_t kv_row
  * nsplit, bit for bit.  Every call on a device shares that device's array:
  * calls that overlap in time on one device (two streams, two threads) race
  * and give wrong results.
- * No counterpart in the reference (its launcher takes caller-owned scratch,
- * P:1235-1241); added for callers that cannot allocate.
+ * No counterpart in the reference; added for callers that cannot allocate.
  */
 int dsa_sparse_mla_decode_noalloc(const void* q_bf16, const void* kv_pool,
                                   int64_t kv_rows, const int32_t* idx,

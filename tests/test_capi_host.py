@@ -162,3 +162,24 @@ def test_sync_status_contract(lib):
     assert f(16, 1, 300000, None, 0, 0, 16, 1, None) == DSA_ERR_INVALID_ARG  # slab too long
     assert f(None, 0, 0, 16, 1, 24, 16, 1, None) == DSA_ERR_INVALID_ARG      # H not a multiple of 16
     assert b"dsa_sync_status" in lib.dsa_last_error()
+
+
+def test_dense_layer_key_count_guard(lib):
+    """A dense layer's key capacity pt_stride*64 must stay <= 2^30 (the same
+    guard as dsa_dense_mla_decode), checked before any launch."""
+    from lagged_indexer_dsa_amd._lib import DSA_ERR_UNSUPPORTED, LayerArgs
+
+    a = LayerArgs()
+    a.q_bf16 = a.kv_pool = a.workspace = a.out_bf16 = a.page_table = a.seq_lens = 16
+    a.kv_rows = 10
+    a.B, a.H, a.topk = 1, 16, 2048
+    a.dense = 1
+    a.pt_stride = (1 << 24) + 1
+    assert lib.dsa_decode_layer(ctypes.byref(a), None) == DSA_ERR_UNSUPPORTED
+    assert b"2^30" in lib.dsa_last_error()
+
+
+def test_layer_args_size_matches_binding(lib):
+    from lagged_indexer_dsa_amd._lib import LayerArgs
+
+    assert lib.dsa_layer_args_bytes() == ctypes.sizeof(LayerArgs)

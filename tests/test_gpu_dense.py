@@ -91,14 +91,18 @@ def _types(n_layers: int, n_dense: int) -> list[bool]:
     return [t is AttentionType.DSA for t in dense_prefix_attention_types(n_layers, n_dense)]
 
 
-@pytest.mark.parametrize("case", ["dense_prefix", "dense_cold_start"])
+@pytest.mark.parametrize("case", ["dense_prefix", "dense_cold_start", "dense_prefix_b8"])
 def test_mli_stack_with_dense_layers(dev, case):
+    """dense_prefix_b8: 8 ragged rows, where each layer runs as three
+    launches (scan, select, then the attention at its own split count), with
+    a dense layer that produces a selection (layer 1) and one that does not
+    (layer 0)."""
     from lagged_indexer_dsa_amd import _lib, ops
     from lagged_indexer_dsa_amd import synthetic as S
     from lagged_indexer_dsa_amd.decode import MLISchedule
 
-    lens = [32768]
-    if case == "dense_prefix":
+    lens = [9000, 3000, 12000, 500, 7000, 2048, 16000, 4097] if case == "dense_prefix_b8" else [32768]
+    if case.startswith("dense_prefix"):
         is_dsa = _types(6, 2)               # F F D D D D
         dense = [not d for d in is_dsa]
     else:
@@ -109,7 +113,7 @@ def test_mli_stack_with_dense_layers(dev, case):
     _lib.sync_timeouts(reset=True)
     pt, num_pages = S.make_page_table(lens, seed=41, device=dev)
     layers = [S.make_decode_layer(lens, seed=420 + i, device=dev, page_table=pt, num_pages=num_pages,
-                                  indexer=produces[i], nsplit=16)
+                                  indexer=produces[i], nsplit=0 if case == "dense_prefix_b8" else 16)
               for i in range(len(is_dsa))]
     for L, d in zip(layers, dense):
         L.dense = d
@@ -132,8 +136,10 @@ def test_mli_stack_with_dense_layers(dev, case):
                                         page_table=pt.cpu().numpy())
                 assert np.array_equal(sels[i].cpu().numpy(), ref_sel), f"{mode} layer {i} selection"
             if dense[i]:
-                err = rel_err(L.out.float().cpu().numpy()[0], _oracle_dense_row(L, 0, lens[0]))
-                assert err < 2e-2, f"{mode} dense layer {i}: rel err {err:.2e}"
+                got = L.out.float().cpu().numpy()
+                for b, n in enumerate(lens):
+                    err = rel_err(got[b], _oracle_dense_row(L, b, n))
+                    assert err < 2e-2, f"{mode} dense layer {i} row {b}: rel err {err:.2e}"
             else:
                 ref = ops.sparse_mla_decode(L.q_bf16, L.kv_pool, sels[src[i]], nsplit=L.nsplit)
                 torch.cuda.synchronize()
