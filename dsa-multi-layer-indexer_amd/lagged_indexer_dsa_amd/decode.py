@@ -24,6 +24,7 @@ import torch
 
 from . import _lib
 from ._lib import LayerArgs
+from .config import AttentionType, ColdStartPolicy, DSAConfig
 from .ops import sparse_mla_workspace, topk_scratch
 
 
@@ -118,6 +119,44 @@ class DecodeLayer:
         _lib.call("dsa_decode_layer", ctypes.byref(a), torch.cuda.current_stream().cuda_stream)
 
 
+@dataclass(frozen=True)
+class LayerPlan:
+    """What one layer does in a decode step under the MLI lag (DSAModel.forward
+    LAGGED_FUSED, model.py:51-71, 104-136): ``dense`` -- it attends its whole
+    prefix (a FULL layer, or layer 0 as a DSA layer under the DENSE cold
+    start); ``indexer`` -- it runs an indexer (iff the next layer is DSA: the
+    lag moves production one layer earlier, so a dense prefix's last FULL
+    layer gains the boundary indexer and the final layer runs none; plus
+    layer 0 under the EAGER cold start, for its own attention);
+    ``attends_own`` -- layer 0 under EAGER attends its own fresh selection."""
+
+    dense: bool
+    indexer: bool
+    attends_own: bool = False
+
+
+def lagged_layer_plan(config: DSAConfig | tuple[AttentionType, ...] | list[AttentionType],
+                      cold_start: ColdStartPolicy = ColdStartPolicy.DENSE) -> list[LayerPlan]:
+    """The per-layer plan of ``config.resolved_attention_types`` (or the
+    types given directly) under the lag and the cold-start policy."""
+    types = config.resolved_attention_types if isinstance(config, DSAConfig) else tuple(config)
+    cold_start = ColdStartPolicy(cold_start)
+    is_dsa = [AttentionType(t) is AttentionType.DSA for t in types]
+    n = len(is_dsa)
+    plan = []
+    for i in range(n):
+        produce = i + 1 < n and is_dsa[i + 1]
+        if not is_dsa[i]:
+            plan.append(LayerPlan(dense=True, indexer=produce))
+        elif i == 0 and cold_start is ColdStartPolicy.DENSE:
+            plan.append(LayerPlan(dense=True, indexer=produce))
+        elif i == 0:  # EAGER: the layer's own indexer feeds its own attention
+            plan.append(LayerPlan(dense=False, indexer=True, attends_own=True))
+        else:
+            plan.append(LayerPlan(dense=False, indexer=produce))
+    return plan
+
+
 def _arg_array(args: list[LayerArgs]):
     arr = (LayerArgs * len(args))()
     for i, a in enumerate(args):
@@ -153,6 +192,27 @@ class MLISchedule:
             self._args.append(layer.args(att, indexer=indexer, attention=attention))
         self._arr = _arg_array(self._args)
         self._graph = None
+
+    @classmethod
+    def for_config(cls, config: DSAConfig | tuple[AttentionType, ...], make_layer, first_attend=None,
+                   cold_start: ColdStartPolicy = ColdStartPolicy.DENSE, lag_depth: int = 1) -> "MLISchedule":
+        """Build a step for a DSA stack: ``make_layer(i, indexer)`` returns
+        layer i's :class:`DecodeLayer` (with indexer operands iff
+        ``indexer``); its dense flag and layer 0's attend set follow
+        :func:`lagged_layer_plan`.  ``first_attend`` is what layer 0 attends
+        when it is a DSA layer without a cold start of its own (not used
+        when layer 0 is dense or attends its own selection)."""
+        plan = lagged_layer_plan(config, cold_start)
+        layers = []
+        for i, p in enumerate(plan):
+            layer = make_layer(i, p.indexer)
+            layer.dense = p.dense
+            layers.append(layer)
+        if plan and (plan[0].dense or plan[0].attends_own):
+            first_attend = layers[0].next_idx  # dense: not read; EAGER: its own fresh selection
+        if first_attend is None:
+            raise ValueError("layer 0 attends first_attend, which is required here")
+        return cls(layers, first_attend, lag_depth=lag_depth)
 
     def run_eager(self) -> None:
         # every buffer the launches touch is owned by the layers, which this

@@ -69,3 +69,30 @@ def test_indexcache_pattern_equals_oracle():
         indexcache_pattern(4, pattern="FX")
     with pytest.raises(ValueError):
         indexcache_pattern(4, freq=0)
+
+
+def test_lagged_layer_plan_follows_the_reference_schedule():
+    """lagged_layer_plan restates DSAModel.forward LAGGED_FUSED (model.py:
+    61-71, 104-136): a layer produces iff the next layer is DSA; FULL layers
+    and a DSA layer 0 under the DENSE cold start attend densely; under EAGER
+    layer 0 runs its own indexer for its own attention."""
+    from lagged_indexer_dsa_amd.config import (AttentionType, ColdStartPolicy, DSAConfig,
+                                               dense_prefix_attention_types)
+    from lagged_indexer_dsa_amd.decode import LayerPlan, lagged_layer_plan
+    from oracle import dsa_oracle as O
+
+    F, D = AttentionType.FULL, AttentionType.DSA
+    for types in ([F, F, D, D, D, D], [D, D, D], [D, F, D, F], [F, F], [D], [D, F, F, D]):
+        for cold in ColdStartPolicy:
+            plan = lagged_layer_plan(tuple(types), cold)
+            prod = O.lagged_indexer_layers([t is D for t in types])
+            for i, (p, t) in enumerate(zip(plan, types)):
+                eager0 = i == 0 and t is D and cold is ColdStartPolicy.EAGER
+                assert p.indexer == (prod[i] or eager0)
+                assert p.dense == (t is F or (i == 0 and t is D and cold is ColdStartPolicy.DENSE))
+                assert p.attends_own == eager0
+    cfg = DSAConfig(num_hidden_layers=6, attention_layer_types=dense_prefix_attention_types(6, 2))
+    assert lagged_layer_plan(cfg) == [LayerPlan(True, False), LayerPlan(True, True)] + \
+        [LayerPlan(False, True)] * 3 + [LayerPlan(False, False)]
+    assert lagged_layer_plan(DSAConfig(num_hidden_layers=3), "eager") == \
+        [LayerPlan(False, True, True), LayerPlan(False, True), LayerPlan(False, False)]

@@ -85,43 +85,42 @@ def test_dense_mla_core_beyond_16k(dev):
         assert rel_err(got[0, s], ref) < 6e-2
 
 
-def _types(n_layers: int, n_dense: int) -> list[bool]:
-    from lagged_indexer_dsa_amd.config import AttentionType, dense_prefix_attention_types
-
-    return [t is AttentionType.DSA for t in dense_prefix_attention_types(n_layers, n_dense)]
-
-
-@pytest.mark.parametrize("case", ["dense_prefix", "dense_cold_start", "dense_prefix_b8"])
+@pytest.mark.parametrize("case", ["dense_prefix", "dense_cold_start", "eager_cold_start", "dense_prefix_b8"])
 def test_mli_stack_with_dense_layers(dev, case):
-    """dense_prefix_b8: 8 ragged rows, where each layer runs as three
-    launches (scan, select, then the attention at its own split count), with
-    a dense layer that produces a selection (layer 1) and one that does not
-    (layer 0)."""
+    """The step built from a config by MLISchedule.for_config.
+    dense_prefix_b8: 8 ragged rows, where each layer runs as three launches
+    (scan, select, then the attention at its own split count), with a dense
+    layer that produces a selection (layer 1) and one that does not (layer
+    0).  eager_cold_start: layer 0 attends its own fresh selection."""
     from lagged_indexer_dsa_amd import _lib, ops
     from lagged_indexer_dsa_amd import synthetic as S
-    from lagged_indexer_dsa_amd.decode import MLISchedule
+    from lagged_indexer_dsa_amd.config import AttentionType, ColdStartPolicy, dense_prefix_attention_types
+    from lagged_indexer_dsa_amd.decode import MLISchedule, lagged_layer_plan
 
     lens = [9000, 3000, 12000, 500, 7000, 2048, 16000, 4097] if case == "dense_prefix_b8" else [32768]
     if case.startswith("dense_prefix"):
-        is_dsa = _types(6, 2)               # F F D D D D
-        dense = [not d for d in is_dsa]
+        types = dense_prefix_attention_types(6, 2)   # F F D D D D
     else:
-        is_dsa = [True] * 4                 # ColdStartPolicy.DENSE: layer 0 attends densely
-        dense = [True, False, False, False]
-    produces = O.lagged_indexer_layers(is_dsa)
-    print(f"[dense] MLI {case} produces={produces}", flush=True)
+        types = (AttentionType.DSA,) * 4
+    cold = ColdStartPolicy.EAGER if case == "eager_cold_start" else ColdStartPolicy.DENSE
+    plan = lagged_layer_plan(types, cold)
+    produces = [p.indexer for p in plan]
+    dense = [p.dense for p in plan]
+    is_dsa = [t is AttentionType.DSA for t in types]
+    assert produces[1:] == O.lagged_indexer_layers(is_dsa)[1:]
+    print(f"[dense] MLI {case} produces={produces} dense={dense}", flush=True)
     _lib.sync_timeouts(reset=True)
     pt, num_pages = S.make_page_table(lens, seed=41, device=dev)
-    layers = [S.make_decode_layer(lens, seed=420 + i, device=dev, page_table=pt, num_pages=num_pages,
-                                  indexer=produces[i], nsplit=0 if case == "dense_prefix_b8" else 16)
-              for i in range(len(is_dsa))]
-    for L, d in zip(layers, dense):
-        L.dense = d
-    # the lagged set of a DSA layer: the previous layer's fresh selection
-    src = [None if dense[i] else i - 1 for i in range(len(is_dsa))]
-    assert all(s is None or produces[s] for s in src), "every DSA layer's predecessor runs an indexer"
-    first = S.random_selection(lens, 2048, pt, seed=97, device=dev)  # ignored: layer 0 is dense
-    sched = MLISchedule(layers, first)
+    nsplit = 0 if case == "dense_prefix_b8" else 16
+    sched = MLISchedule.for_config(
+        types, lambda i, idx: S.make_decode_layer(lens, seed=420 + i, device=dev, page_table=pt,
+                                                  num_pages=num_pages, indexer=idx, nsplit=nsplit),
+        cold_start=cold)
+    layers = sched.layers
+    # the set a sparse layer attends: the previous layer's fresh selection
+    # (layer 0 under EAGER: its own)
+    src = [None if dense[i] else (0 if plan[i].attends_own else i - 1) for i in range(len(types))]
+    assert all(s is None or produces[s] for s in src), "every sparse layer's source runs an indexer"
     for mode in ("eager", "graph", "graph"):
         for L in layers:
             L.out.zero_(); L.next_idx.fill_(-7)
