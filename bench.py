@@ -140,17 +140,38 @@ def speed_of_light(lib, nbytes: int, torch, launches: int = 96) -> dict:
             "read_bytes": nbytes, "read_GBps": round(nbytes / (read_ms * 1e-3) / 1e9, 1)}
 
 
+def kernel_source_sha() -> str:
+    """sha256 (16 hex) over the HIP sources and the C header the library is
+    built from: the kernels' memory traffic is a function of these files."""
+    import hashlib
+
+    h = hashlib.sha256()
+    files = sorted((REPO / "dsa-multi-layer-indexer_amd" / "csrc").glob("*")) + [REPO / "include" / "dsa_mli.h"]
+    for f in files:
+        if f.suffix in (".hip", ".h"):
+            h.update(f.name.encode())
+            h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
 def read_traffic():
     """HBM bytes per fused layer launch measured by the rocprofv3 counter runs
     (FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy) recorded in
-    profiles/; None when that summary is absent."""
+    profiles/, with the kernel-source hash the counters were taken on.
+    Returns (bytes or None, note): None when the summary is absent or was
+    taken on other kernel sources (a stale figure is never reported)."""
     try:
-        for line in TRAFFIC_FILE.read_text().splitlines():
-            if line.startswith("traffic_bytes_per_launch:"):
-                return int(line.split(":", 1)[1].strip())
+        lines = TRAFFIC_FILE.read_text().splitlines()
     except OSError:
-        pass
-    return None
+        return None, "no counter summary"
+    vals = dict(l.split(":", 1) for l in lines if l.startswith(("traffic_bytes_per_launch:", "kernel_source_sha:")))
+    sha = vals.get("kernel_source_sha", "").strip()
+    if sha != kernel_source_sha():
+        return None, f"counter summary taken on kernel sources {sha or '?'}, not these ({kernel_source_sha()})"
+    try:
+        return int(vals["traffic_bytes_per_launch"].strip()), f"rocprofv3 FETCH_SIZE+WRITE_SIZE, sources {sha}"
+    except (KeyError, ValueError):
+        return None, "no traffic line"
 
 
 def cpu_baseline(ctx: int, budget_s: float = 15.0) -> dict:
@@ -268,6 +289,13 @@ def main() -> int:
     scheds = fulls + attn_onlys + idx_onlys
     for s in scheds:
         s.capture()
+    # set-up, not warm-up steps: each graph's first launch (the runtime
+    # uploads the executable graph then) and first touch of its set's
+    # buffers, so that a short run (--steps 20 --warmup 5 touches only a few
+    # of the rotated sets before timing) measures the steady state
+    for s in scheds:
+        s.replay()
+    torch.cuda.synchronize()
 
     def rotated(group):
         state = {"i": 0}
@@ -403,11 +431,33 @@ def main() -> int:
                           "calibration": sol}), flush=True)
         return 0
 
-    reps = max(20, args.steps // 2)
+    # graph steps of the three kinds (a fixed count, after a warm-up of each
+    # kind, so the figure does not depend on --steps)
+    reps = 100
+    for grp in (attn_onlys, idx_onlys, fulls):
+        time_graph(rotated(grp), 2 * n_sets, torch)
     t_attn = time_graph(rotated(attn_onlys), reps, torch)
     t_idx = time_graph(rotated(idx_onlys), reps, torch)
     t_full = time_graph(rotated(fulls), reps, torch)
     hidden = 1.0 - (t_full - t_attn) / t_idx if t_idx > 0 else None
+    # the same from the launches' device time (a graph of back-to-back
+    # launches of one kind, HIP events around it): no step replay overhead
+    import ctypes as _ct
+
+    def layer_launch(kind):
+        argsets = [ls[0].args(first, indexer=(kind != "attn"), attention=(kind != "idx")) for ls in sets]
+        st = {"i": 0}
+
+        def fn():
+            _lib.call("dsa_decode_layer", _ct.byref(argsets[st["i"] % len(argsets)]),
+                      torch.cuda.current_stream().cuda_stream)
+            st["i"] += 1
+        return fn
+    nk = max(48, 2 * n_sets)
+    k_full = graph_event_ms(layer_launch("full"), nk, torch)
+    k_attn = graph_event_ms(layer_launch("attn"), nk, torch)
+    k_idx = graph_event_ms(layer_launch("idx"), nk, torch)
+    hidden_k = 1.0 - (k_full - k_attn) / k_idx if k_idx > 0 else None
     # the same schedule without a graph, over the same rotated sets
     eager_state = {"i": 0}
 
@@ -460,6 +510,7 @@ def main() -> int:
     prep_ms = graph_event_ms(prep, 50, torch)
 
     sol = speed_of_light(_lib.load(), sb, torch)
+    traffic, traffic_note = read_traffic()
     us_layer = ms_step * 1e3 / n_layers
     layer_gbs = lb / (launch_ms * 1e-3) / 1e9
     res = {
@@ -504,10 +555,18 @@ def main() -> int:
                 "hidden_bound": None if t_idx <= 0 else round(min(1.0, t_attn / t_idx), 4),
                 # the other side: the share of the attention's time the step
                 # does not add on top of the indexer alone
-                "attention_hidden_fraction": None if t_attn <= 0 else round(1.0 - (t_full - t_idx) / t_attn, 4)},
+                "attention_hidden_fraction": None if t_attn <= 0 else round(1.0 - (t_full - t_idx) / t_attn, 4),
+                # per launch (device time of back-to-back launches of one
+                # kind): fused layer, attention alone, indexer (scan + select)
+                # alone, and the hidden fraction they give
+                "kernel_us": {"fused": round(k_full * 1e3, 3), "attention_only": round(k_attn * 1e3, 3),
+                              "indexer_only": round(k_idx * 1e3, 3)},
+                "hidden_fraction_kernels": None if hidden_k is None else round(hidden_k, 4),
+                "hidden_bound_kernels": None if k_idx <= 0 else round(min(1.0, k_attn / k_idx), 4)},
         "roofline": {"bound": "hbm", "achieved": round(layer_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(layer_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": read_traffic() if args.config == "c3" else None,
+                     "traffic": traffic if args.config == "c3" and args.scores == "uniform" else None,
+                     "traffic_source": traffic_note,
                      "kernel": "decode_main_kernel (fused layer launch)",
                      "algorithmic_bytes": lb, "launch_us": round(launch_ms * 1e3, 3)},
     }
@@ -518,6 +577,8 @@ def main() -> int:
         return 3
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(131072 if args.config == "c3" else 8192, args.cpu_budget)
+        if args.config == "c3":  # and at C1's context (8192 tokens, the reference's CPU-runnable case)
+            res["cpu_baseline_c1"] = cpu_baseline(8192, min(5.0, args.cpu_budget))
     for s in scheds:
         s.close()
     print(json.dumps(res), flush=True)
