@@ -521,6 +521,7 @@ constexpr int kCoopKeys = 16384;     // positions per workgroup
 constexpr int kCoopMaxBlocks = 256;  // workgroups per row
 constexpr int kPubHdr = 4;           // list header: count, bound key, finite count, max key
 constexpr int kCoopCand = 1024;      // threshold-bin candidates resolved by rank counting
+constexpr int kEmitRegs = 8;         // emit: entries per thread read into registers at once
 struct CoopShared {
   ScanShared scan;
   alignas(16) uint32_t keys[kCoopKeys];
@@ -1218,13 +1219,20 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
       own_ties = __popcll(__ballot(tie && e >= mine0 && e < mine0 + (uint32_t)P));
     } else {
       if (nc <= (uint32_t)kCoopCand) {
+        // rank counting in 16-byte broadcast reads: pad the last uint4 with
+        // 0 (below every candidate)
+        if (t < 3 && nc + (uint32_t)t < (uint32_t)kCoopCand) cs.ck[nc + t] = 0u;
+        __syncthreads();
+        const uint4* c4 = reinterpret_cast<const uint4*>(cs.ck);
+        const int nq = ((int)nc + 3) >> 2;
         for (uint32_t j = t; j < nc; j += kMainThreads) {
           const uint32_t c = cs.ck[j];
           uint32_t gtc = 0, gec = 0;
-          for (uint32_t i = 0; i < nc; ++i) {
-            const uint32_t x = cs.ck[i];
-            gtc += (x > c) ? 1u : 0u;
-            gec += (x >= c) ? 1u : 0u;
+#pragma unroll 4
+          for (int q = 0; q < nq; ++q) {
+            const uint4 x = c4[q];
+            gtc += (x.x > c ? 1u : 0u) + (x.y > c ? 1u : 0u) + (x.z > c ? 1u : 0u) + (x.w > c ? 1u : 0u);
+            gec += (x.x >= c ? 1u : 0u) + (x.y >= c ? 1u : 0u) + (x.z >= c ? 1u : 0u) + (x.w >= c ? 1u : 0u);
           }
           if (gtc < need && need <= gec) {
             cs.res[0] = c;
@@ -1317,6 +1325,46 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
   const int e0 = min(n_e, t * per), e1 = min(n_e, e0 + per);
   const auto entry = [&](int e) { return walk_own ? e : (int)lpos[e]; };  // -> own position index
   uint32_t tie_rank = ties_before;  // rank among all ties of this thread's first tie
+  if (per <= kEmitRegs) {
+    // the thread's entries read into registers at once (all LDS reads in
+    // flight), then ranked and written; key 0 (past the run) is below
+    // every key: never selected, never a tie
+    int ii[kEmitRegs];
+    uint32_t kk[kEmitRegs];
+#pragma unroll
+    for (int j = 0; j < kEmitRegs; ++j) ii[j] = e0 + j < e1 ? entry(e0 + j) : 0;
+#pragma unroll
+    for (int j = 0; j < kEmitRegs; ++j) kk[j] = e0 + j < e1 ? cs.keys[ii[j]] : 0u;
+    uint32_t nt = 0;
+#pragma unroll
+    for (int j = 0; j < kEmitRegs; ++j) nt += (tfin && kk[j] == tstar) ? 1u : 0u;
+    const bool any_tie = own_ties >= 0 ? own_ties > 0 : __syncthreads_or(nt != 0u);
+    if (tfin && any_tie) {
+      uint32_t tot;
+      tie_rank += block_exclusive_scan(nt, cs.wave_tmp, &tot);
+    }
+    uint32_t selm = 0, nmine = 0;
+    {
+      uint32_t tr = tie_rank;
+#pragma unroll
+      for (int j = 0; j < kEmitRegs; ++j) {
+        const bool tie = tfin && kk[j] == tstar;
+        const bool sel = key_is_finite(kk[j]) && (all || kk[j] > tstar || (tie && tr < need3));
+        selm |= sel ? 1u << j : 0u;
+        nmine += sel ? 1u : 0u;
+        tr += tie ? 1u : 0u;
+      }
+    }
+    uint32_t tot_sel;
+    uint32_t pos = base + block_exclusive_scan(nmine, cs.wave_tmp, &tot_sel);
+#pragma unroll
+    for (int j = 0; j < kEmitRegs; ++j)
+      if (selm >> j & 1u) o[min(pos++, (uint32_t)K - 1u)] = slot_of(p_lo + ii[j]);  // < K by construction
+    if (bid == nb - 1)
+      for (int j = (int)nsel + t; j < K; j += kMainThreads) o[j] = TOPK ? S.pad : -1;
+    dbg_stamp(dbk, 11);
+    return;
+  }
   bool any_tie = own_ties > 0;
   if (own_ties < 0) {
     bool has_tie = false;
