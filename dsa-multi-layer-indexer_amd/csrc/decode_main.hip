@@ -381,13 +381,15 @@ __device__ __forceinline__ void attention_block(const AttnArgs& A, int b, int hg
   const int g = t / span;
   constexpr int kLd = 8;                   // partial loads in flight per thread
   float4 x[kLd];
-  // loads past s1 are not issued (s0, s1 are uniform over a wave: its
-  // threads form one group)
+  // loads past s1 read 0: they are issued at the resource's end, so every
+  // load is issued unconditionally and the compiler can wait for the
+  // earlier (m, l) loads alone (a conditional load in between made it wait
+  // for all of them, these partials included)
+  const uint32_t p_end = 16u * (uint32_t)(nsplit * kVec);
   auto load_x = [&](int v, int s0, int s1) {
 #pragma unroll
     for (int i = 0; i < kLd; ++i)
-      x[i] = s0 + i < s1 ? __builtin_bit_cast(float4, load_dev16(prs, 16u * ((s0 + i) * kVec + v)))
-                         : make_float4(0.f, 0.f, 0.f, 0.f);
+      x[i] = __builtin_bit_cast(float4, load_dev16(prs, s0 + i < s1 ? 16u * ((s0 + i) * kVec + v) : p_end));
   };
   {  // the splits' (m, l) first (nsplit*32 floats, <= 8 per thread), then this
      // thread's partials: the merge weights are computed while those arrive
