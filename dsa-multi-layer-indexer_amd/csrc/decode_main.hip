@@ -1089,12 +1089,10 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
   // sel_before = selected above t* before this workgroup, ties_before = ties
   // before it, sel_above = all selected above t*; all: finite counts
   uint32_t sel_before = 0, ties_before = 0, sel_above = 0;
-  int own_ties = -1;  // this workgroup's keys equal to t*, when known here
   const uint32_t mine0 = (uint32_t)(bid * P);
   if (all) {
     sel_before = h0;
     sel_above = h1;
-    own_ties = 0;
   } else {
     // t* must be >= L = the largest list bound for the lists to hold every
     // key >= t*; keys below L never matter.
@@ -1135,7 +1133,6 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
       sel_before = rr.sel_before;
       ties_before = rr.ties_before;
       sel_above = rr.sel_above;
-      own_ties = (int)rr.own_eq;
       radix_own = rr.own_gt + (key_is_finite(tstar) ? min(rr.own_eq, need3 - min(ties_before, need3)) : 0u);
       radix = true;
     } else {
@@ -1218,7 +1215,6 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
       sel_before += (uint32_t)__popcll(__ballot(g && before));
       ties_before = (uint32_t)__popcll(__ballot(tie && before));
       sel_above += (uint32_t)__popcll(__ballot(g));
-      own_ties = __popcll(__ballot(tie && e >= mine0 && e < mine0 + (uint32_t)P));
     } else {
       if (nc <= (uint32_t)kCoopCand) {
         // rank counting in 16-byte broadcast reads: pad the last uint4 with
@@ -1326,84 +1322,87 @@ __device__ __forceinline__ void coop_select(CoopShared& cs, unsigned char* smem,
   const int per = (n_e + kMainThreads - 1) / kMainThreads;
   const int e0 = min(n_e, t * per), e1 = min(n_e, e0 + per);
   const auto entry = [&](int e) { return walk_own ? e : (int)lpos[e]; };  // -> own position index
-  uint32_t tie_rank = ties_before;  // rank among all ties of this thread's first tie
-  if (per <= kEmitRegs) {
-    // the thread's entries read into registers at once (all LDS reads in
-    // flight), then ranked and written; key 0 (past the run) is below
-    // every key: never selected, never a tie
-    int ii[kEmitRegs];
-    uint32_t kk[kEmitRegs];
+  // The thread's entries in blocks of kEmitRegs, every LDS read of a block
+  // issued unconditionally (so all are in flight together); past e1 an
+  // entry reads key 0 (below every key: never selected, never a tie).
+  const int e_last = max(e1 - 1, 0);
+  const auto load_blk = [&](int eb, int (&ii)[kEmitRegs], uint32_t (&kk)[kEmitRegs]) {
 #pragma unroll
-    for (int j = 0; j < kEmitRegs; ++j) ii[j] = e0 + j < e1 ? entry(e0 + j) : 0;
+    for (int j = 0; j < kEmitRegs; ++j) ii[j] = min(entry(min(eb + j, e_last)), kCoopKeys - 1);
 #pragma unroll
-    for (int j = 0; j < kEmitRegs; ++j) kk[j] = e0 + j < e1 ? cs.keys[ii[j]] : 0u;
-    uint32_t nt = 0;
-#pragma unroll
-    for (int j = 0; j < kEmitRegs; ++j) nt += (tfin && kk[j] == tstar) ? 1u : 0u;
-    const bool any_tie = own_ties >= 0 ? own_ties > 0 : __syncthreads_or(nt != 0u);
-    if (tfin && any_tie) {
-      uint32_t tot;
-      tie_rank += block_exclusive_scan(nt, cs.wave_tmp, &tot);
+    for (int j = 0; j < kEmitRegs; ++j) {
+      const uint32_t k = cs.keys[ii[j]];
+      kk[j] = eb + j < e1 ? k : 0u;
     }
-    uint32_t selm = 0, nmine = 0;
-    {
-      uint32_t tr = tie_rank;
+  };
+  // output slots of a block, read unconditionally (page entries of the
+  // workgroup's own pages; a position clamped into the row), so that the
+  // stores after them need not wait for one another
+  const auto slots_blk = [&](const int (&ii)[kEmitRegs], int (&sl)[kEmitRegs]) {
+    if (TOPK && !pt_row) {
+#pragma unroll
+      for (int j = 0; j < kEmitRegs; ++j) sl[j] = p_lo + ii[j];
+    } else if (pts_lds) {
 #pragma unroll
       for (int j = 0; j < kEmitRegs; ++j) {
-        const bool tie = tfin && kk[j] == tstar;
-        const bool sel = key_is_finite(kk[j]) && (all || kk[j] > tstar || (tie && tr < need3));
-        selm |= sel ? 1u << j : 0u;
-        nmine += sel ? 1u : 0u;
-        tr += tie ? 1u : 0u;
+        const int p = p_lo + ii[j];
+        sl[j] = pts[min((p >> 6) - pg0, kScanMaxPages - 1)] * DSA_PAGE_TOKENS + (p & (DSA_PAGE_TOKENS - 1));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kEmitRegs; ++j) {
+        const int p = min(p_lo + ii[j], S.pt_stride * DSA_PAGE_TOKENS - 1);
+        sl[j] = pt_row[p >> 6] * DSA_PAGE_TOKENS + (p & (DSA_PAGE_TOKENS - 1));
       }
     }
-    uint32_t tot_sel;
-    uint32_t pos = base + block_exclusive_scan(nmine, cs.wave_tmp, &tot_sel);
+  };
+  // tr: the rank among the row's ties at t* of the next tie seen
+  const auto is_sel = [&](uint32_t k, uint32_t& tr) {
+    const bool tie = tfin && k == tstar;
+    const bool sel = key_is_finite(k) && (all || k > tstar || (tie && tr < need3));
+    tr += tie ? 1u : 0u;
+    return sel;
+  };
+  // pass 1: the thread's keys above t* and ties at t*; ONE block scan of
+  // both (packed: each count < 2^16) gives the output position: the keys
+  // above t* before this thread plus the ties selected before it (ties are
+  // taken in rank order, the first need3 of the row)
+  int ii[kEmitRegs], sl[kEmitRegs];
+  uint32_t kk[kEmitRegs];
+#pragma unroll
+  for (int j = 0; j < kEmitRegs; ++j) ii[j] = 0, kk[j] = 0u;
+  uint32_t ngt = 0, nt = 0;
+  for (int eb = e0; eb < e1; eb += kEmitRegs) {
+    load_blk(eb, ii, kk);
+#pragma unroll
+    for (int j = 0; j < kEmitRegs; ++j) {
+      ngt += (key_is_finite(kk[j]) && (all || kk[j] > tstar)) ? 1u : 0u;
+      nt += (tfin && kk[j] == tstar) ? 1u : 0u;
+    }
+  }
+  const bool one = per <= kEmitRegs;  // uniform: the block is still in registers
+  if (one && e0 < e1) slots_blk(ii, sl);
+  dbg_stamp(dbk, 32);
+  static_assert(kCoopKeys < 65536, "packed emit counts");
+  uint32_t tot;
+  const uint32_t pk = block_exclusive_scan(ngt | nt << 16, cs.wave_tmp, &tot);
+  dbg_stamp(dbk, 34);
+  uint32_t tr = ties_before + (pk >> 16);
+  uint32_t pos = sel_before + (pk & 0xffffu) + (tfin ? min(tr, need3) : 0u);
+  if (one) {
 #pragma unroll
     for (int j = 0; j < kEmitRegs; ++j)
-      if (selm >> j & 1u) o[min(pos++, (uint32_t)K - 1u)] = slot_of(p_lo + ii[j]);  // < K by construction
-    if (bid == nb - 1)
-      for (int j = (int)nsel + t; j < K; j += kMainThreads) o[j] = TOPK ? S.pad : -1;
-    dbg_stamp(dbk, 11);
-    return;
-  }
-  bool any_tie = own_ties > 0;
-  if (own_ties < 0) {
-    bool has_tie = false;
-    if (tfin)
-      for (int e = e0; e < e1; ++e) has_tie |= cs.keys[entry(e)] == tstar;
-    any_tie = __syncthreads_or(has_tie);
-  }
-  if (tfin && any_tie) {
-    uint32_t nt = 0;
-    for (int e = e0; e < e1; ++e) nt += (cs.keys[entry(e)] == tstar) ? 1u : 0u;
-    uint32_t tot;
-    tie_rank += block_exclusive_scan(nt, cs.wave_tmp, &tot);
-  }
-  uint32_t nmine = 0;
-  {
-    uint32_t tr = tie_rank;
-    for (int e = e0; e < e1; ++e) {
-      const uint32_t k = cs.keys[entry(e)];
-      const bool tie = tfin && k == tstar;
-      nmine += (key_is_finite(k) && (all || k > tstar || (tie && tr < need3))) ? 1u : 0u;
-      tr += tie ? 1u : 0u;
+      if (is_sel(kk[j], tr)) o[min(pos++, (uint32_t)K - 1u)] = sl[j];  // < K by construction
+  } else {
+    for (int eb = e0; eb < e1; eb += kEmitRegs) {
+      load_blk(eb, ii, kk);
+      slots_blk(ii, sl);
+#pragma unroll
+      for (int j = 0; j < kEmitRegs; ++j)
+        if (is_sel(kk[j], tr)) o[min(pos++, (uint32_t)K - 1u)] = sl[j];  // < K by construction
     }
   }
-  uint32_t tot_sel;
-  uint32_t pos = base + block_exclusive_scan(nmine, cs.wave_tmp, &tot_sel);
-  {
-    uint32_t tr = tie_rank;
-    for (int e = e0; e < e1; ++e) {
-      const int i = entry(e);
-      const uint32_t k = cs.keys[i];
-      const bool tie = tfin && k == tstar;
-      if (key_is_finite(k) && (all || k > tstar || (tie && tr < need3))) {
-        o[min(pos++, (uint32_t)K - 1u)] = slot_of(p_lo + i);  // < K by construction
-      }
-      tr += tie ? 1u : 0u;
-    }
-  }
+  dbg_stamp(dbk, 35);
   if (bid == nb - 1)
     for (int j = (int)nsel + t; j < K; j += kMainThreads) o[j] = TOPK ? S.pad : -1;
   dbg_stamp(dbk, 11);
