@@ -40,6 +40,20 @@ def _oracle_scores_row(L, b: int, n: int) -> np.ndarray:
                             local_pt, np.array([n]), n)[0]
 
 
+def _oracle_scores_sample(L, b: int, n: int, npick: int, seed: int):
+    """Oracle scores of npick random 64-token pages of row b (full pages
+    below n): (positions, scores)."""
+    rng = np.random.default_rng(seed)
+    pg = np.sort(rng.choice(n // 64, size=min(npick, n // 64), replace=False))
+    pages = L.index_k[L.page_table[b, torch.from_numpy(pg).to(L.page_table.device)].long()].cpu().numpy()
+    local_pt = np.arange(pg.size, dtype=np.int32)[None, :]
+    m = 64 * pg.size
+    ref = O.indexer_scores(L.q_fp8[b:b + 1].cpu().numpy(), L.w[b:b + 1].cpu().numpy(), pages, local_pt,
+                           np.array([m]), m)[0]
+    pos = (64 * pg[:, None] + np.arange(64)[None, :]).reshape(-1)
+    return pos, ref
+
+
 def _oracle_attention_row(L, b: int, att: torch.Tensor) -> np.ndarray:
     """Oracle sparse MLA of row b over the KV slots att[b] (gathering only
     those rows)."""
@@ -119,8 +133,9 @@ def c4_lens() -> list[int]:
 def test_c4_varlen32_matches_oracle(dev, mode):
     """C4: 32 ragged rows (~2.4M tokens) through the MLI schedule (scan,
     select and attention launches per layer).  Every row's selection is
-    bit-exact; scores and outputs are checked on 4 rows including the
-    longest and the shortest."""
+    bit-exact; scores and outputs are checked in full on 4 rows including
+    the longest and the shortest, and on every row (scores on 8 random
+    pages, the whole attention output) in the first replay."""
     from lagged_indexer_dsa_amd import _lib
     from lagged_indexer_dsa_amd import synthetic as S
     from lagged_indexer_dsa_amd.decode import MLISchedule
@@ -143,6 +158,16 @@ def test_c4_varlen32_matches_oracle(dev, mode):
         assert _lib.sync_timeouts() == 0, "a group wait expired"
         check_layer(layers[0], first, rows, lens, f"{mode} rep {rep} layer 0")
         check_layer(layers[1], layers[0].next_idx, rows, lens, f"{mode} rep {rep} layer 1")
+        if rep == 0:  # every row: sampled scores and the attention output
+            for li, (L, att) in enumerate(((layers[0], first), (layers[1], layers[0].next_idx))):
+                sc = L.scores.cpu().numpy()
+                out = L.out.float().cpu().numpy()
+                for b, n in enumerate(lens):
+                    pos, ref = _oracle_scores_sample(L, b, n, 8, seed=100 * li + b)
+                    err = rel_err(sc[b, pos], ref)
+                    assert err < 1e-4, f"{mode} layer {li} row {b}: scan rel err {err:.2e} (sampled pages)"
+                    err = rel_err(out[b], _oracle_attention_row(L, b, att))
+                    assert err < 2e-2, f"{mode} layer {li} row {b}: attention rel err {err:.2e}"
     sched.close()
     del layers
     torch.cuda.empty_cache()
@@ -153,8 +178,11 @@ def test_c5_61_layers_indexcache_matches_oracle(dev):
     layer (IndexCache 1/4) with the MLI lag, one hipGraph.  Every layer's
     output equals the standalone attention over the selection the oracle's
     schedule names for it (bitwise, same split count), every fresh selection
-    equals the oracle top-k of its scores, and two layers (the first fresh
-    indexer after layer 0 and a reuse layer) match the oracle end to end."""
+    equals the oracle top-k of its scores, every fresh layer's scores match
+    the oracle on 32 random pages (rel 1e-4), every layer's output matches the
+    oracle's sparse MLA over the oracle-named set (rel 2e-2), and two layers
+    (the first fresh indexer after layer 0 and a reuse layer) match the
+    oracle end to end, scores included."""
     from lagged_indexer_dsa_amd import _lib, ops
     from lagged_indexer_dsa_amd import synthetic as S
     from lagged_indexer_dsa_amd.decode import MLISchedule
@@ -192,4 +220,16 @@ def test_c5_61_layers_indexcache_matches_oracle(dev):
     for i in (4, 5):
         att = first if src[i] == -1 else sels[src[i]]
         check_layer(layers[i], att, [0], lens, f"C5 layer {i}")
+    # every fresh layer's scores on 32 random pages against the oracle
+    for i, L in enumerate(layers):
+        if L.has_indexer:
+            pos, ref = _oracle_scores_sample(L, 0, lens[0], 32, seed=i)
+            err = rel_err(L.scores[0].cpu().numpy()[pos], ref)
+            assert err < 1e-4, f"C5 layer {i} scan rel err {err:.2e} (sampled pages)"
+    # every layer's output against the oracle's sparse MLA over the set the
+    # oracle's schedule names for it (gathering only those 2048 rows)
+    for i, L in enumerate(layers):
+        att = first if src[i] == -1 else sels[src[i]]
+        err = rel_err(L.out[0].float().cpu().numpy(), _oracle_attention_row(L, 0, att))
+        assert err < 2e-2, f"C5 layer {i} attention rel err {err:.2e}"
     sched.close()
