@@ -612,6 +612,12 @@ extern "C" int dsa_internal_set_coop_select(int on) {
   return DSA_OK;
 }
 extern "C" int dsa_internal_group_wait_timeouts(int reset) { return dsa::group_wait_timeouts(reset); }
+// Internal: plain scans of >= 2 rows as one index space over all rows (1,
+// default) or per row (0).
+extern "C" int dsa_internal_set_flat_scan(int on) {
+  dsa::set_flat_scan(on);
+  return DSA_OK;
+}
 // Internal test hook: polls before an in-launch wait gives up (n < 0: the
 // default, about a second).  n = 0 makes every wait that is not already
 // satisfied give up at once, so tests can check expiry reporting without a

@@ -1525,6 +1525,7 @@ __device__ __forceinline__ void scan_block(const ScanArgs& S, int row, int bid, 
   const bool with_hist = S.hist != nullptr;
   const int dbk = blockIdx.x;
   dbg_stamp(dbk, 0);
+  dbg_hw_ids();
   const int cap = min(S.slab_stride, S.pt_stride * DSA_PAGE_TOKENS);
   // TOPK (the standalone top-k over given scores): no page table means the
   // output is positions
@@ -2085,8 +2086,19 @@ static hipError_t launch_nhg(dim3 grid, size_t lds, size_t lds_max, hipStream_t 
               : launch_nhg_p<NHG, 0>(grid, lds, lds_max, s, A, n_att, S);
 }
 
+// the plain scan as one index space over every row (scan_flat.hip)
+hipError_t launch_flat_scan(const ScanArgs& S, int B, hipStream_t s);
+constexpr int kFlatScanMaxRows = 1024;
+static int g_flat_scan = 1;  // internal switch: plain scans of >= 2 rows through launch_flat_scan
+void set_flat_scan(int on) { g_flat_scan = on ? 1 : 0; }
+
 hipError_t launch_decode_main(const AttnArgs* A, int B_att, const ScanArgs* S, int B_scan,
                               hipStream_t s) {
+#ifndef DSA_FLAT_MIN_ROWS
+#define DSA_FLAT_MIN_ROWS 2
+#endif
+  if (!A && S && !S->next_idx && !S->hist && g_flat_scan && B_scan >= DSA_FLAT_MIN_ROWS && B_scan <= kFlatScanMaxRows)
+    return launch_flat_scan(*S, B_scan, s);
   const size_t lds_attn = sizeof(AttnShared);
   const size_t lds_coop = std::max(sizeof(CoopShared), (size_t)kRowSelWords * 4);
   const size_t lds_max = std::max(lds_attn, lds_coop);

@@ -178,6 +178,18 @@ __device__ __forceinline__ void dbg_stamp_lane0(int ph) {
 __device__ __forceinline__ void dbg_value(int, int ph, unsigned long long v) {
   if (threadIdx.x == 0) s_dbg_marks[ph] = v;
 }
+// a value recorded by lane 0 of every wave that calls it
+__device__ __forceinline__ void dbg_value_lane0(int ph, unsigned long long v) {
+  if ((threadIdx.x & (kWave - 1)) == 0) s_dbg_marks[ph] = v;
+}
+// the workgroup's XCD (XCC_ID) and hardware id (HW_ID: CU, SIMD, shader
+// engine) into slots 40 and 41
+__device__ __forceinline__ void dbg_hw_ids() {
+  if (threadIdx.x == 0) {
+    s_dbg_marks[40] = (unsigned)__builtin_amdgcn_s_getreg((3 << 11) | 20);   // XCC_ID[3:0]
+    s_dbg_marks[41] = (unsigned)__builtin_amdgcn_s_getreg((31 << 11) | 4);   // HW_ID
+  }
+}
 // every thread of the workgroup calls it once, at the end
 __device__ __forceinline__ void dbg_flush(int blk) {
   __syncthreads();
@@ -188,6 +200,8 @@ constexpr bool kPhaseStamps = false;
 __device__ __forceinline__ void dbg_begin() {}
 __device__ __forceinline__ void dbg_flush(int) {}
 __device__ __forceinline__ void dbg_value(int, int, unsigned long long) {}
+__device__ __forceinline__ void dbg_hw_ids() {}
+__device__ __forceinline__ void dbg_value_lane0(int, unsigned long long) {}
 __device__ __forceinline__ void dbg_stamp(int, int) {}
 __device__ __forceinline__ void dbg_stamp_wave(int, int, int) {}
 __device__ __forceinline__ void dbg_stamp_lane0(int) {}

@@ -63,6 +63,7 @@ hipError_t launch_decode_main(const AttnArgs* A, int B_att, const ScanArgs* S, i
                               hipStream_t s);
 void set_scan_variant(int v);
 void set_coop_select(int on);
+void set_flat_scan(int on);
 void set_scan_blocks_cap(int n);
 int group_wait_timeouts(int reset);
 void set_spin_limit(int n);  // < 0: the default

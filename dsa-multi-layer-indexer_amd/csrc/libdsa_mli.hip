@@ -4,6 +4,7 @@
 // relocatable device code.
 #include "topk.hip"
 #include "decode_main.hip"
+#include "scan_flat.hip"
 #include "quant.hip"
 #include "capi.hip"
 #include "sol.hip"

@@ -113,6 +113,8 @@ def load(path: Path | None = None) -> ctypes.CDLL:
     lib.dsa_internal_set_scan_variant.argtypes = [_i32]
     lib.dsa_internal_set_coop_select.restype = _i32
     lib.dsa_internal_set_coop_select.argtypes = [_i32]
+    lib.dsa_internal_set_flat_scan.restype = _i32
+    lib.dsa_internal_set_flat_scan.argtypes = [_i32]
     lib.dsa_internal_group_wait_timeouts.restype = _i32
     lib.dsa_internal_group_wait_timeouts.argtypes = [_i32]
     lib.dsa_internal_set_spin_limit.restype = _i32
