@@ -216,18 +216,38 @@ int enqueue_layer(const dsa_layer_args* a, const int32_t* attend, bool with_inde
   const bool own = attention && with_indexer && !dense && attend == a->next_idx;
   int rc;
   if (with_indexer && a->B >= kSplitLaunchRows) {
-    // large batches: a plain scan launch (two workgroups per CU) writes the
-    // scores, a select launch loads them, then the attention runs alone at
-    // its own split count (sharing a launch, each role would hold one
-    // workgroup per CU and starve the other)
+    // large batches: a plain scan launch writes the scores, a select launch
+    // loads them; the attention runs in the scan launch (below) or alone
+    // after the select at its own split count
     dsa::ScanArgs P = S;
     P.next_idx = nullptr;
     P.hist = nullptr;
-    rc = hip_status(dsa::launch_decode_main(nullptr, 0, &P, a->B, s), "indexer scan launch");
+    // the attention over a set this layer does not produce (sparse) rides
+    // in the scan launch, on the CUs beside the scan: its gather then
+    // shares the scan's time instead of following the select.  About a
+    // quarter of the CUs for it (measured at 8, 16, 32 and 64 rows: 64
+    // attention workgroups beat 32 and 96-128; C4 with 2 splits per row
+    // 108 against 120 us per layer with the attention launched after the
+    // select), and only when the scan is long next to the attention's share
+    // of keys (the row capacity stands in for the lengths, which are on the
+    // device): 32 rows of 2K-16K tokens ran 77 against 67 us with it.
+    const long att_groups = (long)a->B * (a->H / dsa::kHeadGroup);
+    const long quarter = dsa::device_cu_count() / 4;
+    const int ride_splits = (int)std::min(8L, std::max(1L, quarter / std::max(1L, att_groups)));
+    const long cap_tokens = (long)a->B * std::min((long)a->slab_stride, (long)a->pt_stride * DSA_PAGE_TOKENS);
+    const bool ride = attention && !own && !dense && a->nsplit <= 0 && dsa::flat_scan_on() &&
+                      a->B <= dsa::kFlatRows && att_groups * ride_splits <= quarter &&
+                      cap_tokens >= 20L * att_groups * a->topk;
+    if (ride) {
+      A = make_attn(ride_splits);
+      rc = hip_status(dsa::launch_flat_scan(&A, a->B, P, a->B, s), "indexer scan + attention launch");
+    } else {
+      rc = hip_status(dsa::launch_decode_main(nullptr, 0, &P, a->B, s), "indexer scan launch");
+    }
     if (rc) return rc;
     S.from_scores = 1;
     rc = hip_status(dsa::launch_decode_main(nullptr, 0, &S, a->B, s), "top-k select launch");
-    if (rc || !attention) return rc;
+    if (rc || !attention || ride) return rc;
     if (a->nsplit <= 0) A = make_attn(0);
     return hip_status(dsa::launch_decode_main(&A, a->B, nullptr, 0, s), "attention launch");
   }

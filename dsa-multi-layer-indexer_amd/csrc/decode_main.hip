@@ -58,7 +58,7 @@ constexpr int kMainWaves = kMainThreads / kWave;  // 8
 constexpr int kTile = 16 * kMainWaves;  // 128 keys per tile
 constexpr int kVLd = DSA_LATENT_DIM + 16;  // value tile row stride (bf16): 264 dwords, 8 mod 64 banks
 constexpr int kPLd = kTile + 8;         // probability row stride (bf16)
-constexpr int kHG = 16;                 // heads per group
+constexpr int kHG = kHeadGroup;         // heads per group
 constexpr int kMaxSplit = 128;
 constexpr int kAutoSplitKeys = 64;  // selected keys per split by default
 
@@ -1976,6 +1976,8 @@ hipError_t launch_sync_status(void* topk_scratch, int B_scan, int slab, void* wo
   return hipGetLastError();
 }
 
+static int device_cus();
+int device_cu_count() { return device_cus(); }
 static int device_cus() {
   static int cus = 0;
   if (!cus) {
@@ -2087,10 +2089,11 @@ static hipError_t launch_nhg(dim3 grid, size_t lds, size_t lds_max, hipStream_t 
 }
 
 // the plain scan as one index space over every row (scan_flat.hip)
-hipError_t launch_flat_scan(const ScanArgs& S, int B, hipStream_t s);
-constexpr int kFlatScanMaxRows = 1024;
+hipError_t launch_flat_scan(const AttnArgs* A, int B_att, const ScanArgs& S, int B, hipStream_t s);
+constexpr int kFlatScanMaxRows = kFlatRows;
 static int g_flat_scan = 1;  // internal switch: plain scans of >= 2 rows through launch_flat_scan
 void set_flat_scan(int on) { g_flat_scan = on ? 1 : 0; }
+bool flat_scan_on() { return g_flat_scan != 0; }
 
 hipError_t launch_decode_main(const AttnArgs* A, int B_att, const ScanArgs* S, int B_scan,
                               hipStream_t s) {
@@ -2098,7 +2101,7 @@ hipError_t launch_decode_main(const AttnArgs* A, int B_att, const ScanArgs* S, i
 #define DSA_FLAT_MIN_ROWS 2
 #endif
   if (!A && S && !S->next_idx && !S->hist && g_flat_scan && B_scan >= DSA_FLAT_MIN_ROWS && B_scan <= kFlatScanMaxRows)
-    return launch_flat_scan(*S, B_scan, s);
+    return launch_flat_scan(nullptr, 0, *S, B_scan, s);
   const size_t lds_attn = sizeof(AttnShared);
   const size_t lds_coop = std::max(sizeof(CoopShared), (size_t)kRowSelWords * 4);
   const size_t lds_max = std::max(lds_attn, lds_coop);

@@ -7,6 +7,9 @@
 
 namespace dsa {
 
+constexpr int kHeadGroup = 16;  // attention heads per head group (one MFMA row block)
+constexpr int kFlatRows = 1024;   // rows the flat plain scan takes
+
 // Split-K sparse MLA over the fp8 latent pool (attention role).
 struct AttnArgs {
   const uint16_t* q;     // [B, H, 576] bf16
@@ -71,6 +74,11 @@ void set_spin_limit(int n);  // < 0: the default
 // `groups` attention barrier areas (B * H/16) into *out (device int).
 hipError_t launch_sync_status(void* topk_scratch, int B_scan, int slab, void* workspace, int groups, int* out,
                               int clear, hipStream_t s);
+// Plain scan of 2..1024 rows as one index space (scan_flat.hip); with A,
+// the attention of B_att rows in the same grid, one split per head group.
+hipError_t launch_flat_scan(const AttnArgs* A, int B_att, const ScanArgs& S, int B, hipStream_t s);
+bool flat_scan_on();
+int device_cu_count();
 int attn_auto_nsplit(int topk, int B, int H);
 int attn_fused_nsplit(int topk, int B, int H);
 size_t attn_workspace_bytes(int B, int H, int nsplit);

@@ -47,6 +47,9 @@ struct FlatShared {
   float sbuf[kFlatBufBatches * DSA_PAGE_TOKENS];  // the share's scores, written out at the end
 };
 
+static_assert(sizeof(FlatShared) <= 160 * 1024, "the flat scan's LDS fits one CU");
+static size_t lds_flat_max() { return std::max(sizeof(FlatShared), sizeof(AttnShared)); }
+
 // largest r in [0, n) with pre[r] <= v (pre[0] == 0 <= v)
 __device__ __forceinline__ int flat_row_of(const int* pre, int n, int v) {
   int lo = 0, hi = n - 1;
@@ -58,10 +61,27 @@ __device__ __forceinline__ int flat_row_of(const int* pre, int n, int v) {
   return lo;
 }
 
-template <int NHG, int VARIANT>
-__global__ void __launch_bounds__(kFlatThreads) flat_scan_kernel(const ScanArgs S, int B) {
+// ATTN: workgroups [0, n_att) run the attention role (one split per (row,
+// head group): no split exchange) over a selection this launch does not
+// produce, beside the scan on the other CUs (one workgroup per CU each:
+// the attention's LDS and registers), so that the attention's gather and
+// the scan's stream share the launch instead of following each other.
+template <int NHG, int VARIANT, bool ATTN>
+__global__ void __launch_bounds__(kFlatThreads) flat_scan_kernel(const AttnArgs A, int n_att, const ScanArgs S,
+                                                                 int B) {
   constexpr int kHeads = NHG * 16;
-  __shared__ FlatShared fs;
+  extern __shared__ __align__(16) unsigned char smem[];
+  if constexpr (ATTN) {
+    if ((int)blockIdx.x < n_att) {
+      dbg_begin();
+      const int nhg = A.H / kHG;
+      const int bid = blockIdx.x;
+      attention_block<false>(A, bid / (A.nsplit * nhg), (bid / A.nsplit) % nhg, bid % A.nsplit, smem);
+      dbg_flush(blockIdx.x);
+      return;
+    }
+  }
+  FlatShared& fs = *reinterpret_cast<FlatShared*>(smem);
   const int t = threadIdx.x;
   const int lane = t & (kWave - 1);
   const int wv = t / kWave;
@@ -122,7 +142,7 @@ __global__ void __launch_bounds__(kFlatThreads) flat_scan_kernel(const ScanArgs 
     }
     __syncthreads();
   }
-  const int nwg = gridDim.x, w = blockIdx.x;
+  const int nwg = (int)gridDim.x - n_att, w = (int)blockIdx.x - n_att;
   const int NB = fs.bpre[B], NT = fs.tpre[B];
   const int b0 = (int)((long)NB * w / nwg), nr = (int)((long)NB * (w + 1) / nwg) - b0;
 
@@ -239,17 +259,17 @@ __global__ void __launch_bounds__(kFlatThreads) flat_scan_kernel(const ScanArgs 
     else if (g < S.slab_stride) S.scores[(long)x.r * S.slab_stride + g] = v;
   };
   // ping-pong over two batches' registers
-  Batch A, Bn;
+  Batch X0, X1;
   int i = take();
-  if (i < nr) issue(i, A);
+  if (i < nr) issue(i, X0);
   while (i < nr) {
     const int j = take();
-    if (j < nr) issue(j, Bn);
-    score(A);
+    if (j < nr) issue(j, X1);
+    score(X0);
     if (j >= nr) break;
     i = take();
-    if (i < nr) issue(i, A);
-    score(Bn);
+    if (i < nr) issue(i, X0);
+    score(X1);
   }
 
   // ---- the staged scores, a row's run at a time ----
@@ -290,28 +310,46 @@ __global__ void __launch_bounds__(kFlatThreads) flat_scan_kernel(const ScanArgs 
   dbg_flush(blockIdx.x);
 }
 
-template <int NHG>
-static void launch_flat(dim3 grid, dim3 block, hipStream_t s, const ScanArgs& S, int B) {
-  if (g_scan_variant == 0) hipLaunchKernelGGL((flat_scan_kernel<NHG, 0>), grid, block, 0, s, S, B);
-  else hipLaunchKernelGGL((flat_scan_kernel<NHG, 1>), grid, block, 0, s, S, B);
+template <int NHG, bool ATTN>
+static hipError_t launch_flat(dim3 grid, size_t lds, hipStream_t s, const AttnArgs& A, int n_att, const ScanArgs& S,
+                              int B) {
+  static bool attr_set = false;  // one host thread per device (as launch_k)
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)flat_scan_kernel<NHG, 0, ATTN>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_flat_max());
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute((const void*)flat_scan_kernel<NHG, 1, ATTN>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_flat_max());
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  if (g_scan_variant == 0)
+    hipLaunchKernelGGL((flat_scan_kernel<NHG, 0, ATTN>), grid, dim3(kFlatThreads), lds, s, A, n_att, S, B);
+  else
+    hipLaunchKernelGGL((flat_scan_kernel<NHG, 1, ATTN>), grid, dim3(kFlatThreads), lds, s, A, n_att, S, B);
+  return hipGetLastError();
 }
 
-// Plain scan launch: one 1024-thread workgroup per CU (more when a share
-// would exceed the LDS page table).
-hipError_t launch_flat_scan(const ScanArgs& S, int B, hipStream_t s) {
+// Plain scan launch: one 512-thread workgroup per CU the attention leaves
+// (more when a share would exceed the LDS page table); with A, B_att
+// attention rows (one split each) in the same grid first.
+hipError_t launch_flat_scan(const AttnArgs* A, int B_att, const ScanArgs& S, int B, hipStream_t s) {
   const long cap = std::min((long)S.slab_stride, (long)S.pt_stride * DSA_PAGE_TOKENS);
   const long max_batches = (long)B * ((cap + DSA_PAGE_TOKENS - 1) / DSA_PAGE_TOKENS);
   if (B > kFlatMaxRows || max_batches >= (1L << 31) || (long)B * S.slab_stride >= (1L << 31))
     return hipErrorInvalidValue;
-  const int nwg = (int)std::max<long>(device_cus(), (max_batches + kFlatMaxPages - 1) / kFlatMaxPages);
-  const dim3 grid(nwg), block(kFlatThreads);
+  const int n_att = A ? B_att * (A->H / kHG) * A->nsplit : 0;
+  const int nwg = (int)std::max<long>(std::max(device_cus() - n_att, device_cus() / 2),
+                                      (max_batches + kFlatMaxPages - 1) / kFlatMaxPages);
+  const dim3 grid(n_att + nwg);
+  const size_t lds = A ? lds_flat_max() : sizeof(FlatShared);
+  const AttnArgs a = A ? *A : AttnArgs{};
   switch (S.Hidx / 16) {
-    case 1: launch_flat<1>(grid, block, s, S, B); break;
-    case 2: launch_flat<2>(grid, block, s, S, B); break;
-    case 3: launch_flat<3>(grid, block, s, S, B); break;
-    default: launch_flat<4>(grid, block, s, S, B);
+    case 1: return A ? launch_flat<1, true>(grid, lds, s, a, n_att, S, B) : launch_flat<1, false>(grid, lds, s, a, 0, S, B);
+    case 2: return A ? launch_flat<2, true>(grid, lds, s, a, n_att, S, B) : launch_flat<2, false>(grid, lds, s, a, 0, S, B);
+    case 3: return A ? launch_flat<3, true>(grid, lds, s, a, n_att, S, B) : launch_flat<3, false>(grid, lds, s, a, 0, S, B);
+    default: return A ? launch_flat<4, true>(grid, lds, s, a, n_att, S, B) : launch_flat<4, false>(grid, lds, s, a, 0, S, B);
   }
-  return hipGetLastError();
 }
 
 }  // namespace dsa
