@@ -224,8 +224,10 @@ int dsa_sparse_mla_decode_noalloc(const void* q_bf16, const void* kv_pool,
  * (4) One DSA decode layer on one stream:
  *   indexer scan -> top-k (position order, KV-slot output into next_idx),
  *   and attention over attend_idx (the lagged set: the attention and the
- *   scan then share ONE launch; from B = 8 rows the scan, the select and
- *   the attention are three launches in that order), or over this layer's own
+ *   scan then share ONE launch; from B = 8 rows the scan launch carries
+ *   the attention on about a quarter of the CUs when the rows' capacity is
+ *   large next to B * topk, and the select follows; else scan, select and
+ *   attention are three launches in that order), or over this layer's own
  *   fresh selection when attend_idx == NULL (baseline DSA: scan, select,
  *   then attention).
  * scores [B, slab_stride] fp32 scratch; next_idx [B, topk] int32.
@@ -274,8 +276,9 @@ int dsa_decode_layer(const dsa_layer_args* args, void* stream);
  * an indexer (its attend_idx when given; layer 0 must be given one, unless
  * it is dense), or densely when its `dense` flag is set, and
  * layer i's indexer scan runs in the SAME launch as layer i's attention
- * (role-decoupled workgroups; from B = 8 rows scan, select and attention
- * are three launches), followed by layer i's
+ * (role-decoupled workgroups; from B = 8 rows the scan launch carries the
+ * attention and the select follows, or the three run as separate launches),
+ * followed by layer i's
  * top-k select, which layer i+1 attends.  A layer whose q_fp8 is NULL runs no indexer (IndexCache
  * reuse); one whose q_bf16 is NULL runs no attention.  Everything is on one
  * stream: the overlap of indexer and attention is inside each launch.
