@@ -11,7 +11,7 @@
 // Work layout.  Row b's positions are cut into batches of 64 tokens (one
 // index-K page, 4 chunks of 16 keys; the last batch of a row is partly
 // past len_b).  The batches of all rows, row after row, form one index
-// space; workgroup w (512 threads, one per CU: 146 VGPRs) takes the w-th
+// space; workgroup w (512 threads, one per CU: its LDS) takes the w-th
 // equal share of it, and its 8 waves take the batches of that share one at
 // a time from an LDS counter, each keeping its next batch's loads in flight
 // while it scores the current one.  Measured on the per-row form (two
@@ -61,11 +61,14 @@ __device__ __forceinline__ int flat_row_of(const int* pre, int n, int v) {
   return lo;
 }
 
-// ATTN: workgroups [0, n_att) run the attention role (one split per (row,
-// head group): no split exchange) over a selection this launch does not
-// produce, beside the scan on the other CUs (one workgroup per CU each:
-// the attention's LDS and registers), so that the attention's gather and
-// the scan's stream share the launch instead of following each other.
+// ATTN: workgroups [0, n_att) run the attention role (A.nsplit splits per
+// (row, head group), merged as in the decode launch) over a selection this
+// launch does not produce, beside the scan on the other CUs (one workgroup
+// per CU each: the LDS), so that the attention's gather and the scan's
+// stream share the launch instead of following each other.  Attention
+// workgroups come first in the grid, so a (row, head group)'s splits are
+// resident together (their merge waits for each other); the scan's never
+// wait.
 template <int NHG, int VARIANT, bool ATTN>
 __global__ void __launch_bounds__(kFlatThreads) flat_scan_kernel(const AttnArgs A, int n_att, const ScanArgs S,
                                                                  int B) {
@@ -87,8 +90,10 @@ __global__ void __launch_bounds__(kFlatThreads) flat_scan_kernel(const AttnArgs 
   const int wv = t / kWave;
   const int kr = lane & 15, kc = lane >> 4;
   const int cap = min(S.slab_stride, S.pt_stride * DSA_PAGE_TOKENS);
-  dbg_begin();
-  __syncthreads();
+  if constexpr (kPhaseStamps) {
+    dbg_begin();
+    __syncthreads();
+  }
   dbg_stamp(0, 0);
   dbg_hw_ids();
 
