@@ -6,9 +6,10 @@ splits per (row, head group)) when the rows' capacity is large next to
 B * topk; the select follows as its own launch.  Checked here against the
 oracle and against the standalone attention, bitwise, at the split count
 the launch used (one of 2, 4, 8): 16 and 32 heads (one and two head
-groups), 8 and 16 rows, a short row among long ones, an attend set with
-padding (-1) entries, two replays of the same layer (the scratch re-arms
-itself), selections bit-exact against the oracle's top-k of the scores.
+groups), 8 and 16 rows, a short row among long ones, an empty row and a
+row shorter than top-k, an attend set with padding (-1) entries, two
+replays of the same layer (the scratch re-arms itself), selections
+bit-exact against the oracle's top-k of the scores.
 """
 
 from __future__ import annotations
@@ -36,6 +37,8 @@ CASES = [
     ("b8_h16", [100000, 90000, 120000, 85000, 131072, 95000, 110000, 3000], 16),
     ("b8_h32", [100000, 90000, 120000, 85000, 131072, 95000, 110000, 99000], 32),
     ("b16_h16", [int(x) for x in np.random.default_rng(16).integers(60000, 131073, 16)], 16),
+    # an empty row and a row shorter than top-k among long ones
+    ("b8_empty_short", [120000, 0, 131072, 1500, 100000, 110000, 125000, 90000], 16),
 ]
 
 
