@@ -567,8 +567,10 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(layer_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(layer_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic if args.config == "c3" and args.scores == "uniform" else None,
-                     "traffic_source": traffic_note,
-                     "kernel": "decode_main_kernel (fused layer launch)",
+                     "traffic_source": traffic_note if args.config == "c3" and args.scores == "uniform"
+                     else "the counter summary covers the C3 launch only",
+                     "kernel": "decode_main_kernel (fused layer launch)" if B < 8 else
+                     "flat_scan_kernel (scan, attention riding) + decode_main_kernel (select): the layer's launches",
                      "algorithmic_bytes": lb, "launch_us": round(launch_ms * 1e3, 3)},
     }
     n_timeouts = _lib.sync_timeouts()
