@@ -1978,14 +1978,17 @@ hipError_t launch_sync_status(void* topk_scratch, int B_scan, int slab, void* wo
 
 static int device_cus();
 int device_cu_count() { return device_cus(); }
+// the current device's CU count (devices 0-63 cached)
 static int device_cus() {
-  static int cus = 0;
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  const bool keep = dev >= 0 && dev < 64;
+  int cus = keep ? cached[dev].load(std::memory_order_relaxed) : 0;
   if (!cus) {
-    int dev = 0;
     hipDeviceProp_t prop;
-    cus = (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess)
-              ? prop.multiProcessorCount
-              : 256;
+    cus = hipGetDeviceProperties(&prop, dev) == hipSuccess ? prop.multiProcessorCount : 256;
+    if (keep) cached[dev].store(cus, std::memory_order_relaxed);
   }
   return cus;
 }
@@ -2046,13 +2049,12 @@ int scan_blocks_per_row(int B, int pt_stride, int slab_stride, int att_blocks, b
 template <int NHG, int VARIANT, int ROLES>
 static hipError_t launch_k(dim3 grid, size_t lds, size_t lds_max, hipStream_t s, const AttnArgs& A,
                            int n_att, const ScanArgs& S) {
-  static bool attr_set = false;  // one host thread per device (the reference's K:2506-2522 rule)
-  if (!attr_set) {
-    const hipError_t e = hipFuncSetAttribute((const void*)decode_main_kernel<NHG, VARIANT, ROLES>,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_max);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static PerDeviceOnce attr;
+  const hipError_t e = attr.run([lds_max] {
+    return hipFuncSetAttribute((const void*)decode_main_kernel<NHG, VARIANT, ROLES>,
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_max);
+  });
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((decode_main_kernel<NHG, VARIANT, ROLES>), grid, dim3(kMainThreads), lds, s, A, n_att, S);
   return hipGetLastError();
 }

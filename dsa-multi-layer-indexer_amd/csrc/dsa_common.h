@@ -4,11 +4,29 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <type_traits>
 
 #include "dsa_mli.h"
 
 namespace dsa {
+
+// Host side: a set-up step (a kernel's LDS attribute) that must run once per
+// device, on the first launch with that device current.  Devices 0-63 are
+// remembered; any other device runs the step on every launch.
+struct PerDeviceOnce {
+  std::atomic<uint64_t> done{0};
+  template <class F>
+  hipError_t run(F&& step) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    const uint64_t bit = (dev >= 0 && dev < 64) ? (1ull << dev) : 0ull;
+    if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
+    const hipError_t e = step();
+    if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_release);
+    return e;
+  }
+};
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));

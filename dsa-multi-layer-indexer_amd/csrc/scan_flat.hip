@@ -318,16 +318,16 @@ __global__ void __launch_bounds__(kFlatThreads) flat_scan_kernel(const AttnArgs 
 template <int NHG, bool ATTN>
 static hipError_t launch_flat(dim3 grid, size_t lds, hipStream_t s, const AttnArgs& A, int n_att, const ScanArgs& S,
                               int B) {
-  static bool attr_set = false;  // one host thread per device (as launch_k)
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)flat_scan_kernel<NHG, 0, ATTN>,
+  static PerDeviceOnce attr;
+  const hipError_t e = attr.run([] {
+    hipError_t r = hipFuncSetAttribute((const void*)flat_scan_kernel<NHG, 0, ATTN>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_flat_max());
-    if (e == hipSuccess)
-      e = hipFuncSetAttribute((const void*)flat_scan_kernel<NHG, 1, ATTN>,
+    if (r == hipSuccess)
+      r = hipFuncSetAttribute((const void*)flat_scan_kernel<NHG, 1, ATTN>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_flat_max());
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+    return r;
+  });
+  if (e != hipSuccess) return e;
   if (g_scan_variant == 0)
     hipLaunchKernelGGL((flat_scan_kernel<NHG, 0, ATTN>), grid, dim3(kFlatThreads), lds, s, A, n_att, S, B);
   else

@@ -681,14 +681,12 @@ hipError_t launch_topk_hist(const float* scores, const int* seq_lens, void* scra
 hipError_t launch_topk_select(const float* scores, const int* seq_lens, const int* page_table,
                               int pt_stride, void* scratch, int* out, int B, int slab, int K,
                               int sorted, int pad, hipStream_t s) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)topk_select_kernel,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)sizeof(FinShared));
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static PerDeviceOnce attr;
+  const hipError_t e = attr.run([] {
+    return hipFuncSetAttribute((const void*)topk_select_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)sizeof(FinShared));
+  });
+  if (e != hipSuccess) return e;
   const dim3 slices((slab + kSlice - 1) / kSlice, B);
   hipLaunchKernelGGL(topk_select_kernel, slices, dim3(kSliceThreads), sizeof(FinShared), s, scores,
                      seq_lens, page_table, pt_stride, reinterpret_cast<uint32_t*>(scratch), out,
