@@ -140,17 +140,20 @@ def speed_of_light(lib, nbytes: int, torch, launches: int = 96) -> dict:
             "read_bytes": nbytes, "read_GBps": round(nbytes / (read_ms * 1e-3) / 1e9, 1)}
 
 
-def kernel_source_sha() -> str:
+def kernel_source_sha(root: Path = REPO) -> str:
     """sha256 (16 hex) over the HIP sources and the C header the library is
-    built from: the kernels' memory traffic is a function of these files."""
+    built from, comments and whitespace left out: the kernels' memory
+    traffic is a function of this code, not of its comments."""
     import hashlib
+    import re
 
     h = hashlib.sha256()
-    files = sorted((REPO / "dsa-multi-layer-indexer_amd" / "csrc").glob("*")) + [REPO / "include" / "dsa_mli.h"]
+    files = sorted((root / "dsa-multi-layer-indexer_amd" / "csrc").glob("*")) + [root / "include" / "dsa_mli.h"]
     for f in files:
         if f.suffix in (".hip", ".h"):
+            code = re.sub(r"//[^\n]*|/\*.*?\*/", " ", f.read_text(), flags=re.S)
             h.update(f.name.encode())
-            h.update(f.read_bytes())
+            h.update(" ".join(code.split()).encode())
     return h.hexdigest()[:16]
 
 

@@ -16,7 +16,10 @@
  *     DSA_ERR_HIP when the HIP launch itself failed;
  *     dsa_last_error() returns a message for the calling thread;
  *   - per-row context lengths are read from device memory (`seq_lens`), so a
- *     captured launch replays correctly as contexts grow.
+ *     captured launch replays correctly as contexts grow;
+ *   - work goes to the calling thread's current device; the library's own
+ *     per-device state (kernel LDS attributes, CU counts, the static array of
+ *     the allocation-free entry point) is set up on a device's first call.
  *
  * Data layouts in HBM (shared by all entry points):
  *   index-K page  : 8448 bytes = [64 keys x 128 B e4m3][64 x fp32 key scale]
