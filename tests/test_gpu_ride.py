@@ -8,7 +8,8 @@ oracle and against the standalone attention, bitwise, at the split count
 the launch used (one of 2, 4, 8): 16 and 32 heads (one and two head
 groups), 8 and 16 rows, a short row among long ones, an empty row and a
 row shorter than top-k, an attend set with padding (-1) entries, two
-replays of the same layer (the scratch re-arms itself), selections
+replays of the same layer (the scratch re-arms itself), every score the
+same bits as the plain scan launch's (the scores start as NaN), selections
 bit-exact against the oracle's top-k of the scores.
 """
 
@@ -53,12 +54,16 @@ def test_riding_attention_matches_oracle(dev, name, lens, heads):
     L = S.make_decode_layer(lens, seed=52, device=dev, page_table=pt, num_pages=num_pages, heads=heads)
     att = S.random_selection(lens, 2048, pt, seed=53, device=dev)
     att[0, -100:] = -1  # padding entries in the attended set
+    plain = ops.indexer_scan(L.q_fp8, L.w, L.index_k, L.page_table, L.seq_lens, L.slab_stride).view(torch.int32)
     for rep in range(2):
         L.out.zero_()
         L.next_idx.fill_(-7)
+        L.scores.fill_(float("nan"))
         L.run(attend_idx=att)
         torch.cuda.synchronize()
         assert _lib.sync_timeouts() == 0, "a group wait expired"
+        # every score written, the same bits as the plain scan launch
+        assert torch.equal(L.scores.view(torch.int32), plain), f"rep {rep}: scores"
         ref_sel = O.topk_select(L.scores.cpu().numpy(), np.array(lens), L.topk, page_table=pt.cpu().numpy())
         assert np.array_equal(L.next_idx.cpu().numpy(), ref_sel), f"rep {rep}: selection"
         got = L.out.view(torch.int16)
