@@ -166,7 +166,10 @@ __global__ void __launch_bounds__(kFlatThreads) flat_scan_kernel(const AttnArgs 
   // scan ~13% (79 against 69 us with the stores left out; non-temporal
   // stores: the same 79): a share that fits the LDS buffer keeps its scores
   // there and writes them out at the end as 16-byte stores of contiguous
-  // runs (C4's scan 79.0 -> 74.6 us).
+  // runs (C4's scan 79.0 -> 74.6 us).  Those end-of-launch stores, and the
+  // -inf tails after them, are non-temporal: written as ordinary stores
+  // they sat dirty in the L2s, whose write-back the launch's end then
+  // waited for (C4's scan 75.6 -> 72.0 us, its layer ~109 -> ~104 us).
   const bool staged = nr <= kFlatBufBatches;
 
   // ---- the waves take the share's batches; each wave keeps the next
@@ -289,9 +292,9 @@ __global__ void __launch_bounds__(kFlatThreads) flat_scan_kernel(const AttnArgs 
       float* dst = S.scores + (long)r * S.slab_stride;
       if (S.slab_stride % 4 == 0) {  // 16-byte stores (p0, p1 and the row start are multiples of 4)
         for (int p = p0 + 4 * t; p < p1; p += 4 * kFlatThreads)
-          *reinterpret_cast<float4*>(dst + p) = *reinterpret_cast<const float4*>(src + p);
+          __builtin_nontemporal_store(*reinterpret_cast<const v4f*>(src + p), reinterpret_cast<v4f*>(dst + p));
       } else {
-        for (int p = p0 + t; p < p1; p += kFlatThreads) dst[p] = src[p];
+        for (int p = p0 + t; p < p1; p += kFlatThreads) __builtin_nontemporal_store(src[p], dst + p);
       }
     }
   }
@@ -305,7 +308,7 @@ __global__ void __launch_bounds__(kFlatThreads) flat_scan_kernel(const AttnArgs 
         const int s0 = max(t0, fs.tpre[r]), s1 = min(t1, fs.tpre[r + 1]);
         const int base = min((fs.bpre[r + 1] - fs.bpre[r]) * DSA_PAGE_TOKENS, S.slab_stride) - fs.tpre[r];
         float* srow = S.scores + (long)r * S.slab_stride + base;
-        for (int p = s0 + t; p < s1; p += kFlatThreads) srow[p] = -INFINITY;
+        for (int p = s0 + t; p < s1; p += kFlatThreads) __builtin_nontemporal_store(-INFINITY, srow + p);
       }
     }
   }
