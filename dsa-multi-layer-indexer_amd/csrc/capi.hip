@@ -236,7 +236,7 @@ int enqueue_layer(const dsa_layer_args* a, const int32_t* attend, bool with_inde
     const int ride_splits = (int)std::min(8L, std::max(1L, quarter / std::max(1L, att_groups)));
     const long cap_tokens = (long)a->B * std::min((long)a->slab_stride, (long)a->pt_stride * DSA_PAGE_TOKENS);
     const bool ride = attention && !own && !dense && a->nsplit <= 0 && dsa::flat_scan_on() &&
-                      a->B <= dsa::kFlatRows && att_groups * ride_splits <= quarter &&
+                      dsa::flat_scan_fits(P, a->B) && att_groups * ride_splits <= quarter &&
                       cap_tokens >= 20L * att_groups * a->topk;
     if (ride) {
       A = make_attn(ride_splits);

@@ -2102,7 +2102,7 @@ hipError_t launch_decode_main(const AttnArgs* A, int B_att, const ScanArgs* S, i
 #ifndef DSA_FLAT_MIN_ROWS
 #define DSA_FLAT_MIN_ROWS 2
 #endif
-  if (!A && S && !S->next_idx && !S->hist && g_flat_scan && B_scan >= DSA_FLAT_MIN_ROWS && B_scan <= kFlatScanMaxRows)
+  if (!A && S && !S->next_idx && !S->hist && g_flat_scan && B_scan >= DSA_FLAT_MIN_ROWS && flat_scan_fits(*S, B_scan))
     return launch_flat_scan(nullptr, 0, *S, B_scan, s);
   const size_t lds_attn = sizeof(AttnShared);
   const size_t lds_coop = std::max(sizeof(CoopShared), (size_t)kRowSelWords * 4);

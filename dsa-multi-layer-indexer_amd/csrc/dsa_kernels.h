@@ -75,8 +75,10 @@ void set_spin_limit(int n);  // < 0: the default
 hipError_t launch_sync_status(void* topk_scratch, int B_scan, int slab, void* workspace, int groups, int* out,
                               int clear, hipStream_t s);
 // Plain scan of 2..1024 rows as one index space (scan_flat.hip); with A,
-// the attention of B_att rows in the same grid, one split per head group.
+// the attention of B_att rows in the same grid (A->nsplit splits per row
+// and head group).
 hipError_t launch_flat_scan(const AttnArgs* A, int B_att, const ScanArgs& S, int B, hipStream_t s);
+bool flat_scan_fits(const ScanArgs& S, int B);
 bool flat_scan_on();
 int device_cu_count();
 int attn_auto_nsplit(int topk, int B, int H);

@@ -338,14 +338,22 @@ static hipError_t launch_flat(dim3 grid, size_t lds, hipStream_t s, const AttnAr
   return hipGetLastError();
 }
 
-// Plain scan launch: one 512-thread workgroup per CU the attention leaves
-// (more when a share would exceed the LDS page table); with A, B_att
-// attention rows (one split each) in the same grid first.
-hipError_t launch_flat_scan(const AttnArgs* A, int B_att, const ScanArgs& S, int B, hipStream_t s) {
+// Whether B rows fit the flat scan's index spaces (batches and tail
+// positions counted in 32-bit ints, row prefixes held in LDS).
+bool flat_scan_fits(const ScanArgs& S, int B) {
   const long cap = std::min((long)S.slab_stride, (long)S.pt_stride * DSA_PAGE_TOKENS);
   const long max_batches = (long)B * ((cap + DSA_PAGE_TOKENS - 1) / DSA_PAGE_TOKENS);
-  if (B > kFlatMaxRows || max_batches >= (1L << 31) || (long)B * S.slab_stride >= (1L << 31))
-    return hipErrorInvalidValue;
+  return B >= 1 && B <= kFlatMaxRows && max_batches < (1L << 31) && (long)B * S.slab_stride < (1L << 31);
+}
+
+// Plain scan launch: one 512-thread workgroup per CU the attention leaves
+// (more when a share would exceed the LDS page table); with A, the
+// attention of B_att rows (A->nsplit splits per row and head group) in the
+// same grid first.
+hipError_t launch_flat_scan(const AttnArgs* A, int B_att, const ScanArgs& S, int B, hipStream_t s) {
+  if (!flat_scan_fits(S, B)) return hipErrorInvalidValue;
+  const long cap = std::min((long)S.slab_stride, (long)S.pt_stride * DSA_PAGE_TOKENS);
+  const long max_batches = (long)B * ((cap + DSA_PAGE_TOKENS - 1) / DSA_PAGE_TOKENS);
   const int n_att = A ? B_att * (A->H / kHG) * A->nsplit : 0;
   const int nwg = (int)std::max<long>(std::max(device_cus() - n_att, device_cus() / 2),
                                       (max_batches + kFlatMaxPages - 1) / kFlatMaxPages);
