@@ -171,6 +171,8 @@ __global__ void __launch_bounds__(kFlatThreads) flat_scan_kernel(const AttnArgs 
   // they sat dirty in the L2s, whose write-back the launch's end then
   // waited for (C4's scan 75.6 -> 72.0 us, its layer ~109 -> ~104 us).
   const bool staged = nr <= kFlatBufBatches;
+  // rows start on 16-byte boundaries: the staged runs go out as 16-byte stores
+  const bool vec = S.slab_stride % 4 == 0 && ((uintptr_t)S.scores & 15) == 0;
 
   // ---- the waves take the share's batches; each wave keeps the next
   // batch's loads in flight while it scores the current one ----
@@ -290,7 +292,7 @@ __global__ void __launch_bounds__(kFlatThreads) flat_scan_kernel(const AttnArgs 
       const int p1 = min((be - fs.bpre[r]) * DSA_PAGE_TOKENS, S.slab_stride);
       const float* src = fs.sbuf + (bs - b0) * DSA_PAGE_TOKENS - p0;
       float* dst = S.scores + (long)r * S.slab_stride;
-      if (S.slab_stride % 4 == 0) {  // 16-byte stores (p0, p1 and the row start are multiples of 4)
+      if (vec) {  // 16-byte stores (p0, p1 and the row start are multiples of 4)
         for (int p = p0 + 4 * t; p < p1; p += 4 * kFlatThreads)
           __builtin_nontemporal_store(*reinterpret_cast<const v4f*>(src + p), reinterpret_cast<v4f*>(dst + p));
       } else {

@@ -131,3 +131,26 @@ def test_flat_scan_c4_rows(dev):
                                64 * pg.size)[0]
         pos = (64 * pg[:, None] + np.arange(64)[None, :]).reshape(-1)
         assert C.rel_err(sc[b, pos].astype(np.float64), ref) < 1e-4, f"row {b}"
+
+
+def test_flat_scan_output_not_16_byte_aligned(dev):
+    """A score slab starting 4 bytes past a 16-byte boundary (a view one
+    float into a buffer): every row start is then off the 16-byte grid, so
+    the staged runs go out as 4-byte stores; the same bits as an aligned
+    slab, -inf tails included, and the float before the slab untouched."""
+    from lagged_indexer_dsa_amd import ops
+
+    lens = [300, 1000, 64, 0, 777]
+    print(f"[scan-flat] unaligned output lens={lens}", flush=True)
+    case = C.index_case(seed=11, lens=lens, hidx=64)
+    slab = case["pt"].shape[1] * 64
+    d = C.to_dev(case, dev)
+    ref = _scan(d, slab, 1)
+    big = torch.full((len(lens) * slab + 1,), 7.0, device=dev)
+    out = big[1:].view(len(lens), slab)
+    assert out.data_ptr() % 16 == 4
+    ops.indexer_scan(d["q"], d["w"], d["pages"], d["pt"], d["lens"], slab, out=out)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    assert big[0].item() == 7.0
+
